@@ -1,0 +1,148 @@
+// attn_tile.h -- one wave computes sparse attention for one query (gfx950).
+//
+//   sel(s)   = s <= t  &&  score[s] >= thr                (dsa_attention.py:45-46, :258)
+//   O[h,:]   = sum_{s in sel} softmax_s(<Q[t,h],K[s,h]> * scale) * V[s,h,:]
+//
+// The wave scans the score row 256 entries at a time (a float4 per lane),
+// compacts the selected key positions in index order into a per-wave LDS
+// list (ballot-free: a wave prefix sum of per-lane counts), then gathers
+// only those K/V rows.  Each K (or V) row is HQ*D contiguous elements; lane
+// l owns elements [l*EK, (l+1)*EK) -- one 16-byte-granular contiguous slice,
+// so a row gather is a single coalesced wave load.  Per-head logits are a
+// butterfly over the DQ/EK lanes of the head.  Softmax is online (running
+// max m, normaliser l) in the log2 domain with fp32 state, so the whole
+// selected set is never materialised and any selected count works -- ties at
+// the threshold can select more than k keys (the reference keeps ties).
+#pragma once
+
+#include "dsa_device.h"
+
+namespace dsa {
+
+constexpr int kListCap = 256;  // one 256-entry segment of the score row
+
+// Q/K/V point at this batch element: Q row t is Q + t*HQ*DQ, etc.
+// load4(s, sv) loads scores s..s+3 (s <= t, s % 4 == 0) of this query's row.
+template <typename Tag, int EK, int EV, typename Load4>
+__device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict__ Q,
+                                             const typename Tag::raw* __restrict__ K,
+                                             const typename Tag::raw* __restrict__ V, int t,
+                                             int HQ, int DQ, int DV, float scale_log2,
+                                             float thr, Load4&& load4, int* list,
+                                             float* __restrict__ out_row) {
+  using raw = typename Tag::raw;
+  const int lane = lane_id();
+  const int EQ = HQ * DQ;
+  const int EVt = HQ * DV;
+  const bool kact = lane * EK < EQ;
+  const bool vact = lane * EV < EVt;
+  const int lphk = DQ / EK;                     // lanes per head, K side
+  const int hv = (lane * EV) / DV;              // head of this lane's V slice
+  const int src_lane = (hv * lphk) & (kWave - 1);
+  const bool same_map = (DQ / EK) == (DV / EV);  // K and V slices cover the same head
+
+  float q[EK];
+  if (kact) {
+    load_cvt<Tag, EK>(Q + static_cast<int64_t>(t) * EQ + lane * EK, q);
+#pragma unroll
+    for (int e = 0; e < EK; ++e) q[e] *= scale_log2;
+  } else {
+#pragma unroll
+    for (int e = 0; e < EK; ++e) q[e] = 0.f;
+  }
+  float acc[EV];
+#pragma unroll
+  for (int e = 0; e < EV; ++e) acc[e] = 0.f;
+  float m = -__builtin_huge_valf();
+  float lsum = 0.f;
+
+  // Logit (log2 domain) of key s for this lane's V head.
+  auto process = [&](const int* ss, int nu) {
+    constexpr int U = (EK <= 8) ? 4 : 2;
+    float kv[U][EK];
+    float vv[U][EV];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (u < nu) {
+        const int64_t s = ss[u];
+        if (kact) load_cvt<Tag, EK>(K + s * EQ + lane * EK, kv[u]);
+        else {
+#pragma unroll
+          for (int e = 0; e < EK; ++e) kv[u][e] = 0.f;
+        }
+        if (vact) load_cvt<Tag, EV>(V + s * EVt + lane * EV, vv[u]);
+        else {
+#pragma unroll
+          for (int e = 0; e < EV; ++e) vv[u][e] = 0.f;
+        }
+      }
+    }
+    float lg[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < EK; ++e) d = fmaf(q[e], kv[u][e], d);
+      lg[u] = d;
+    }
+    for (int o = 1; o < lphk; o <<= 1) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) lg[u] += __shfl_xor(lg[u], o, kWave);
+    }
+    if (!same_map) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) lg[u] = __shfl(lg[u], src_lane, kWave);
+    }
+    float mnew = m;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (u < nu) mnew = fmaxf(mnew, lg[u]);
+    const float alpha = exp2f(m - mnew);
+    lsum *= alpha;
+#pragma unroll
+    for (int e = 0; e < EV; ++e) acc[e] *= alpha;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (u < nu) {
+        const float p = exp2f(lg[u] - mnew);
+        lsum += p;
+#pragma unroll
+        for (int e = 0; e < EV; ++e) acc[e] = fmaf(p, vv[u][e], acc[e]);
+      }
+    }
+    m = mnew;
+  };
+
+  for (int s0 = 0; s0 <= t; s0 += 4 * kWave) {
+    const int sb = s0 + 4 * lane;
+    float sv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (sb <= t) load4(sb, sv);
+    int cnt = 0;
+    bool keep[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      keep[c] = (sb + c <= t) && (sv[c] >= thr);
+      cnt += keep[c] ? 1 : 0;
+    }
+    const int incl = wave_inclusive_sum(cnt);
+    const int total = __shfl(incl, kWave - 1, kWave);
+    int p = incl - cnt;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (keep[c]) list[p++] = sb + c;
+    wave_lds_sync();
+    constexpr int U = (EK <= 8) ? 4 : 2;
+    int i = 0;
+    for (; i + U <= total; i += U) process(list + i, U);
+    for (; i < total; ++i) process(list + i, 1);
+    wave_lds_sync();
+  }
+
+  if (vact) {
+    const float inv = 1.f / lsum;  // lsum == 0 only if nothing passed: NaN, as the reference
+#pragma unroll
+    for (int e = 0; e < EV; ++e) out_row[lane * EV + e] = acc[e] * inv;
+  }
+}
+
+}  // namespace dsa

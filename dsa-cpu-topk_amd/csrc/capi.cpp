@@ -1,0 +1,144 @@
+// capi.cpp -- the exported C ABI (include/dsa_amd.h): argument validation,
+// error reporting and dispatch to the gfx950 launchers.
+//
+// Every check runs before the first HIP call, so invalid arguments are
+// reported (negative status + message) on a machine without a GPU.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/dsa_amd.h"
+#include "dsa_launch.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return DSA_OK;
+  return fail(DSA_EHIP, "%s: HIP error %d (%s)", what, static_cast<int>(e), hipGetErrorString(e));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+bool dtype_ok(int d) { return d == DSA_F32 || d == DSA_BF16 || d == DSA_F16; }
+
+// Elements of a 16-bit or 32-bit tensor fit the 32-bit indices some kernels use.
+constexpr int64_t kMaxElems = (int64_t{1} << 31) - 1;
+
+int check_indexer(const void* q, const void* k, const void* w, int dtype, int64_t B, int64_t T,
+                  int HI, int DI, const float* scores, int64_t ld) {
+  if (!dtype_ok(dtype)) return fail(DSA_EINVAL, "indexer: unknown dtype %d", dtype);
+  if (B < 0 || T < 0) return fail(DSA_EINVAL, "indexer: negative size B=%lld T=%lld", (long long)B, (long long)T);
+  if (T > kMaxElems) return fail(DSA_EINVAL, "indexer: T=%lld too large", (long long)T);
+  if (HI < 1 || HI > 256) return fail(DSA_EINVAL, "indexer: HI=%d outside [1,256]", HI);
+  if (ld < T) return fail(DSA_EINVAL, "indexer: ld=%lld < T=%lld", (long long)ld, (long long)T);
+  if (!dsa::indexer_supported(dtype, DI))
+    return fail(DSA_EUNSUPPORTED, "indexer: DI=%d unsupported for dtype %d (fp32: 16..256, 16-bit: 32..256, powers of two)", DI, dtype);
+  if (B * T == 0) return DSA_OK;
+  if (!q || !k || !w || !scores) return fail(DSA_EINVAL, "indexer: null pointer");
+  if (!aligned16(q) || !aligned16(k)) return fail(DSA_EINVAL, "indexer: q_idx/k_idx must be 16-byte aligned");
+  if (B * T * HI * static_cast<int64_t>(DI) > (int64_t{1} << 40)) return fail(DSA_EINVAL, "indexer: q_idx too large");
+  return DSA_OK;
+}
+
+int check_attn(int dtype, int64_t B, int64_t T, int HQ, int DQ, int DV, const void* Q,
+               const void* K, const void* V, const float* out, const char* who) {
+  if (!dtype_ok(dtype)) return fail(DSA_EINVAL, "%s: unknown dtype %d", who, dtype);
+  if (B < 0 || T < 0) return fail(DSA_EINVAL, "%s: negative size", who);
+  if (T > kMaxElems) return fail(DSA_EINVAL, "%s: T=%lld too large", who, (long long)T);
+  if (!pow2(HQ) || !pow2(DQ) || !pow2(DV))
+    return fail(DSA_EINVAL, "%s: HQ=%d DQ=%d DV=%d must be powers of 2", who, HQ, DQ, DV);
+  if (!dsa::sparse_attn_supported(dtype, HQ, DQ, DV))
+    return fail(DSA_EUNSUPPORTED, "%s: no kernel for HQ=%d DQ=%d DV=%d dtype %d", who, HQ, DQ, DV, dtype);
+  if (B * T == 0) return DSA_OK;
+  if (!Q || !K || !V || !out) return fail(DSA_EINVAL, "%s: null pointer", who);
+  if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(out))
+    return fail(DSA_EINVAL, "%s: Q/K/V/out must be 16-byte aligned", who);
+  return DSA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* dsa_last_error(void) { return g_err; }
+
+const char* dsa_version(void) { return "dsa_amd 0.1.0 gfx950"; }
+
+int64_t dsa_fused_max_T(void) { return dsa::kFusedMaxT; }
+
+int dsa_indexer_scores(const void* q_idx, const void* k_idx, const void* w_idx, int dtype,
+                       int64_t B, int64_t T, int HI, int DI, float* scores, int64_t ld,
+                       int write_upper, void* stream) {
+  int rc = check_indexer(q_idx, k_idx, w_idx, dtype, B, T, HI, DI, scores, ld);
+  if (rc != DSA_OK || B * T == 0) return rc;
+  return hip_status(dsa::launch_indexer(q_idx, k_idx, w_idx, dtype, B, T, HI, DI, scores, ld,
+                                        write_upper, static_cast<hipStream_t>(stream)),
+                    "dsa_indexer_scores");
+}
+
+int dsa_topk_threshold(const float* scores, int64_t rows, int64_t n, int64_t ld, int k,
+                       int64_t causal_T, float* thr, int32_t* idx, void* stream) {
+  if (rows < 0 || n < 0) return fail(DSA_EINVAL, "topk: negative size rows=%lld n=%lld", (long long)rows, (long long)n);
+  if (k <= 0) return fail(DSA_EINVAL, "topk: k must be > 0 (got %d)", k);
+  if (k > n) return fail(DSA_EINVAL, "topk: k must be <= N (k=%d, N=%lld)", k, (long long)n);
+  if (n > kMaxElems) return fail(DSA_EINVAL, "topk: row length %lld >= 2^31", (long long)n);
+  if (rows > kMaxElems) return fail(DSA_EINVAL, "topk: %lld rows >= 2^31", (long long)rows);
+  if (ld < n) return fail(DSA_EINVAL, "topk: ld=%lld < N=%lld", (long long)ld, (long long)n);
+  if (causal_T < 0) return fail(DSA_EINVAL, "topk: causal_T=%lld < 0", (long long)causal_T);
+  if (causal_T > 0) {
+    if (causal_T > n) return fail(DSA_EINVAL, "topk: causal_T=%lld > N=%lld", (long long)causal_T, (long long)n);
+    if (rows % causal_T != 0) return fail(DSA_EINVAL, "topk: rows=%lld not a multiple of causal_T=%lld", (long long)rows, (long long)causal_T);
+  }
+  if (rows == 0) return DSA_OK;
+  if (!scores || !thr) return fail(DSA_EINVAL, "topk: null pointer");
+  return hip_status(dsa::launch_topk(scores, rows, n, ld, k, causal_T, thr, idx,
+                                     static_cast<hipStream_t>(stream)),
+                    "dsa_topk_threshold");
+}
+
+int dsa_sparse_attn_threshold(const float* scores, int64_t ld, const float* thr, const void* Q,
+                              const void* K, const void* V, int dtype, int64_t B, int64_t T,
+                              int HQ, int DQ, int DV, float scale, float* out, void* stream) {
+  int rc = check_attn(dtype, B, T, HQ, DQ, DV, Q, K, V, out, "sparse_attn");
+  if (rc != DSA_OK) return rc;
+  if (ld < T) return fail(DSA_EINVAL, "sparse_attn: ld=%lld < T=%lld", (long long)ld, (long long)T);
+  if (!std::isfinite(scale)) return fail(DSA_EINVAL, "sparse_attn: scale must be finite");
+  if (B * T == 0) return DSA_OK;
+  if (!scores || !thr) return fail(DSA_EINVAL, "sparse_attn: null pointer");
+  return hip_status(dsa::launch_sparse_attn(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, DV,
+                                            scale, out, static_cast<hipStream_t>(stream)),
+                    "dsa_sparse_attn_threshold");
+}
+
+int dsa_fused_forward(const void* q_idx, const void* k_idx, const void* w_idx, const void* Q,
+                      const void* K, const void* V, int dtype, int64_t B, int64_t T, int HI,
+                      int DI, int HQ, int DQ, int DV, int top_k, float scale, float* out,
+                      void* stream) {
+  if (T > dsa::kFusedMaxT)
+    return fail(DSA_EUNSUPPORTED, "fused: T=%lld > %lld (use the split pipeline)", (long long)T, (long long)dsa::kFusedMaxT);
+  if (top_k < 1) return fail(DSA_EINVAL, "fused: top_k must be >= 1 (got %d)", top_k);
+  int rc = check_indexer(q_idx, k_idx, w_idx, dtype, B, T, HI, DI, out, T);
+  if (rc != DSA_OK) return rc;
+  rc = check_attn(dtype, B, T, HQ, DQ, DV, Q, K, V, out, "fused");
+  if (rc != DSA_OK) return rc;
+  if (!std::isfinite(scale)) return fail(DSA_EINVAL, "fused: scale must be finite");
+  if (B * T == 0) return DSA_OK;
+  hipError_t e = dsa::launch_fused(q_idx, k_idx, w_idx, Q, K, V, dtype, B, T, HI, DI, HQ, DQ,
+                                   DV, top_k, scale, out, static_cast<hipStream_t>(stream));
+  if (e == hipErrorNotSupported)
+    return fail(DSA_EUNSUPPORTED, "fused: no fused instance for dtype %d DI=%d HQ=%d DQ=%d DV=%d", dtype, DI, HQ, DQ, DV);
+  return hip_status(e, "dsa_fused_forward");
+}
+
+}  // extern "C"

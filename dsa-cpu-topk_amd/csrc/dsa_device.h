@@ -1,0 +1,181 @@
+// dsa_device.h -- device helpers shared by the gfx950 DSA kernels.
+//
+// Wave64 primitives, the order-preserving float -> uint32 radix key, MFMA
+// operand types, and typed loads.  Written for CDNA4 (gfx950) only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dsa {
+
+constexpr int kWave = 64;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// Storage tags for the three input element types.  Arithmetic is fp32 always.
+struct F32 { using raw = float; static constexpr int kBytes = 4; };
+struct BF16 { using raw = uint16_t; static constexpr int kBytes = 2; };
+struct F16 { using raw = uint16_t; static constexpr int kBytes = 2; };
+
+__device__ __forceinline__ float to_f32(F32, float x) { return x; }
+__device__ __forceinline__ float to_f32(BF16, uint16_t x) {
+  return __uint_as_float(static_cast<uint32_t>(x) << 16);
+}
+__device__ __forceinline__ float to_f32(F16, uint16_t x) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, x));
+}
+
+// ---------------------------------------------------------------------------
+// Radix keys.  Unsigned order of the key equals the numeric order of the
+// float, with -0.0 folded onto +0.0 (IEEE '>=' treats them as equal, and the
+// reference selects with '>=': dsa_attention.py:46) and every NaN folded onto
+// one positive quiet NaN that ranks above +inf (torch.topk's NaN order).
+// -inf maps to 0x007FFFFF, the smallest key a float can produce; key 0 is
+// therefore free and marks "no element" (padding, masked positions).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t float_to_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  u = (u == 0x80000000u) ? 0u : u;
+  u = ((u & 0x7fffffffu) > 0x7f800000u) ? 0x7fc00000u : u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_to_float(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+constexpr uint32_t kKeyNone = 0u;
+
+// ---------------------------------------------------------------------------
+// Wave64 primitives.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+// Orders this wave's LDS traffic: everything issued before is visible to every
+// lane of the wave after.  (A wave's LDS instructions complete in order; the
+// fence makes the compiler wait for them and not move accesses across.)
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_inclusive_sum(T v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    T t = __shfl_up(v, o, kWave);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ uint32_t popc64(uint64_t m) {
+  return static_cast<uint32_t>(__popcll(m));
+}
+// Number of set bits of m below this lane.
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+}
+
+// Block-wide exclusive prefix sum in thread order (NT threads, NT % 64 == 0).
+// wsum must hold NT/64 words of LDS.  Contains two __syncthreads().
+template <int NT>
+__device__ __forceinline__ uint32_t block_exclusive_sum(uint32_t v, uint32_t* wsum,
+                                                        uint32_t& total) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  const uint32_t incl = wave_inclusive_sum(v);
+  if (lane == kWave - 1) wsum[wid] = incl;
+  __syncthreads();
+  uint32_t base = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < NT / kWave; ++w) {
+    const uint32_t s = wsum[w];
+    base += (w < wid) ? s : 0u;
+    tot += s;
+  }
+  __syncthreads();
+  total = tot;
+  return base + incl - v;
+}
+
+// ---------------------------------------------------------------------------
+// Typed vector loads: N consecutive elements starting at p (N*bytes a multiple
+// of 16 and p 16-byte aligned when vec is true) converted to fp32.
+// ---------------------------------------------------------------------------
+template <int N>
+__device__ __forceinline__ void load_f32(const float* __restrict__ p, float (&out)[N]) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(p + i);
+      out[i] = v.x; out[i + 1] = v.y; out[i + 2] = v.z; out[i + 3] = v.w;
+    }
+  } else if constexpr (N % 2 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 2) {
+      const float2 v = *reinterpret_cast<const float2*>(p + i);
+      out[i] = v.x; out[i + 1] = v.y;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = p[i];
+  }
+}
+
+template <typename Tag, int N>
+__device__ __forceinline__ void load_cvt(const typename Tag::raw* __restrict__ p, float (&out)[N]) {
+  if constexpr (Tag::kBytes == 4) {
+    load_f32<N>(reinterpret_cast<const float*>(p), out);
+  } else {
+    if constexpr (N % 8 == 0) {
+#pragma unroll
+      for (int i = 0; i < N; i += 8) {
+        const uint4 v = *reinterpret_cast<const uint4*>(p + i);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          out[i + 2 * j] = to_f32(Tag{}, static_cast<uint16_t>(w[j] & 0xffffu));
+          out[i + 2 * j + 1] = to_f32(Tag{}, static_cast<uint16_t>(w[j] >> 16));
+        }
+      }
+    } else if constexpr (N % 2 == 0) {
+#pragma unroll
+      for (int i = 0; i < N; i += 2) {
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(p + i);
+        out[i] = to_f32(Tag{}, static_cast<uint16_t>(w & 0xffffu));
+        out[i + 1] = to_f32(Tag{}, static_cast<uint16_t>(w >> 16));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) out[i] = to_f32(Tag{}, p[i]);
+    }
+  }
+}
+
+// XCD-aware block order.  Workgroups are dispatched round-robin over the 8
+// XCDs (block i runs on XCD i % 8).  Remap so that XCD x works through a
+// contiguous range of logical blocks -- neighbouring logical blocks share K/V
+// rows and hit the same L2.  Identity when nblocks is not a multiple of 8.
+__device__ __forceinline__ uint32_t xcd_swizzle(uint32_t bid, uint32_t nblocks) {
+  if ((nblocks & 7u) != 0u) return bid;
+  return (bid & 7u) * (nblocks >> 3) + (bid >> 3);
+}
+
+}  // namespace dsa

@@ -1,0 +1,35 @@
+// dsa_launch.h -- internal host-side launchers (C++ linkage, not exported).
+// capi.cpp validates arguments and then calls these; each one enqueues its
+// kernels on `stream` and returns the launch status.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dsa {
+
+// Radix-select: thr[r] = k-th largest of row r, optional exactly-k indices.
+hipError_t launch_topk(const float* scores, int64_t rows, int64_t n, int64_t ld, int k,
+                       int64_t causal_T, float* thr, int32_t* idx, hipStream_t stream);
+
+// Lightning indexer.  dtype: 0 f32, 1 bf16, 2 f16.
+hipError_t launch_indexer(const void* q, const void* k, const void* w, int dtype, int64_t B,
+                          int64_t T, int HI, int DI, float* scores, int64_t ld,
+                          int write_upper, hipStream_t stream);
+bool indexer_supported(int dtype, int DI);
+
+// Threshold-driven sparse attention.
+hipError_t launch_sparse_attn(const float* scores, int64_t ld, const float* thr, const void* Q,
+                              const void* K, const void* V, int dtype, int64_t B, int64_t T,
+                              int HQ, int DQ, int DV, float scale, float* out,
+                              hipStream_t stream);
+bool sparse_attn_supported(int dtype, int HQ, int DQ, int DV);
+
+// Fused forward for T <= kFusedMaxT.
+constexpr int64_t kFusedMaxT = 2048;
+hipError_t launch_fused(const void* qi, const void* ki, const void* wi, const void* Q,
+                        const void* K, const void* V, int dtype, int64_t B, int64_t T, int HI,
+                        int DI, int HQ, int DQ, int DV, int top_k, float scale, float* out,
+                        hipStream_t stream);
+
+}  // namespace dsa

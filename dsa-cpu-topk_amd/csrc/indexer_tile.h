@@ -1,0 +1,166 @@
+// indexer_tile.h -- one wave's lightning-indexer tile on MFMA (gfx950).
+//
+//   I[t,s] = sum_j w[t,j] * ReLU(<q[t,j,:], k[s,:]>)      (lightning_indexer.py:26-33)
+//
+// A wave owns 4 consecutive queries t0..t0+3 and walks the keys in blocks of
+// 16.  The GEMM rows are (query, head) pairs, 4 queries x 4 heads = 16 rows
+// per MFMA, one MFMA row-group per group of 4 heads ("head group", hg).  With
+// that row order the 16x16 MFMA output layout puts all 4 heads of one
+// (query, key) pair in the 4 accumulator registers of one lane:
+//     lane l  ->  query t0 + l/16, key s0 + l%16, heads 4hg..4hg+3
+// so the ReLU * w head reduction is 4 v_max + 4 v_fma per lane per head
+// group, entirely in registers -- no shuffles, no LDS.
+//
+// The reduction dimension DI is permuted so every lane's operand slice is
+// contiguous in memory: lane group g = l/16 owns dims [g*DI/4, (g+1)*DI/4),
+// and MFMA step kk consumes element kk (fp32, K=4 per MFMA) or elements
+// 8kk..8kk+7 (bf16/fp16, K=32 per MFMA) of that slice.  A and B use the same
+// permutation, so the sum over DI is unchanged and each lane loads its slice
+// with 16-byte vector loads.
+//
+//   fp32 inputs : v_mfma_f32_16x16x4_f32     (exact fp32 products, fp32 sum)
+//   bf16 inputs : v_mfma_f32_16x16x32_bf16   (exact products, fp32 sum)
+//   fp16 inputs : v_mfma_f32_16x16x32_f16
+#pragma once
+
+#include "dsa_device.h"
+
+namespace dsa {
+
+// Per-lane operand slice of DI/4 elements in MFMA-ready registers.
+template <typename Tag, int E>
+struct Slice;
+
+template <int E>
+struct Slice<F32, E> {
+  static constexpr int kSteps = E;  // one MFMA per element
+  float v[E];
+  __device__ __forceinline__ void load(const float* __restrict__ p) { load_f32<E>(p, v); }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < E; ++i) v[i] = 0.f;
+  }
+  __device__ __forceinline__ f32x4 mfma(int i, const Slice& b, f32x4 acc) const {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(v[i], b.v[i], acc, 0, 0, 0);
+  }
+};
+
+template <typename Tag, int E>
+struct Slice16 {
+  static_assert(E % 8 == 0, "16-bit slices are whole 8-element MFMA operands");
+  static constexpr int kSteps = E / 8;
+  uint4 v[E / 8];
+  __device__ __forceinline__ void load(const uint16_t* __restrict__ p) {
+#pragma unroll
+    for (int i = 0; i < E / 8; ++i) v[i] = *reinterpret_cast<const uint4*>(p + 8 * i);
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < E / 8; ++i) v[i] = make_uint4(0u, 0u, 0u, 0u);
+  }
+};
+
+template <int E>
+struct Slice<BF16, E> : Slice16<BF16, E> {
+  __device__ __forceinline__ f32x4 mfma(int i, const Slice& b, f32x4 acc) const {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, this->v[i]),
+                                                   __builtin_bit_cast(bf16x8, b.v[i]), acc, 0,
+                                                   0, 0);
+  }
+};
+
+template <int E>
+struct Slice<F16, E> : Slice16<F16, E> {
+  __device__ __forceinline__ f32x4 mfma(int i, const Slice& b, f32x4 acc) const {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, this->v[i]),
+                                                  __builtin_bit_cast(f16x8, b.v[i]), acc, 0, 0,
+                                                  0);
+  }
+};
+
+// Computes scores of queries t0..t0+3 (batch row base pointers given) against
+// keys [s_begin, s_end) in super-blocks of 16*KB keys and hands each finished
+// super-block to sink(s0, sc) where lane l holds sc[kb] = score of query
+// t0 + l/16 and key s0 + 16*kb + l%16.  Entries with key > query, key >= T or
+// query >= T hold garbage/-inf; the sink applies the causal mask and bounds.
+//
+// q : [T, HI, DI] of this batch element   k : [T, DI]   w : [T, HI]
+template <typename Tag, int DI, int KB, typename Sink>
+__device__ __forceinline__ void indexer_rows(const typename Tag::raw* __restrict__ q,
+                                             const typename Tag::raw* __restrict__ k,
+                                             const typename Tag::raw* __restrict__ w, int T,
+                                             int HI, int t0, int s_begin, int s_end,
+                                             Sink&& sink) {
+  constexpr int E = DI / 4;
+  using S = Slice<Tag, E>;
+  const int lane = lane_id();
+  const int g = lane >> 4;   // lane group: reduction slice; output query
+  const int r16 = lane & 15; // A row / B column
+  const int nhg = (HI + 3) >> 2;
+
+  // A row of this lane: query t0 + r16/4, head 4*hg + r16%4.
+  const int qa = t0 + (r16 >> 2);
+  const int ha = r16 & 3;
+  // Output query of this lane.
+  const int qo = t0 + g;
+
+  // Head-group-invariant operands when HI <= 4: load once.
+  S a_cached;
+  float w_cached[4];
+  auto load_a = [&](int hg, S& a, float (&wv)[4]) {
+    const int head = 4 * hg + ha;
+    if (qa < T && head < HI)
+      a.load(q + (static_cast<int64_t>(qa) * HI + head) * DI + g * E);
+    else
+      a.zero();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int hw = 4 * hg + r;
+      wv[r] = (qo < T && hw < HI) ? to_f32(Tag{}, w[static_cast<int64_t>(qo) * HI + hw]) : 0.f;
+    }
+  };
+  if (nhg == 1) load_a(0, a_cached, w_cached);
+
+  for (int s0 = s_begin; s0 < s_end; s0 += 16 * KB) {
+    S bk[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      const int s = s0 + 16 * kb + r16;
+      if (s < T)
+        bk[kb].load(k + static_cast<int64_t>(s) * DI + g * E);
+      else
+        bk[kb].zero();
+    }
+    float sc[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) sc[kb] = 0.f;
+
+    for (int hg = 0; hg < nhg; ++hg) {
+      S a;
+      float wv[4];
+      if (nhg == 1) {
+        a = a_cached;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wv[r] = w_cached[r];
+      } else {
+        load_a(hg, a, wv);
+      }
+      f32x4 acc[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) acc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < S::kSteps; ++i) {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) acc[kb] = a.mfma(i, bk[kb], acc[kb]);
+      }
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[kb] = fmaf(wv[r], fmaxf(acc[kb][r], 0.f), sc[kb]);
+      }
+    }
+    sink(s0, sc);
+  }
+}
+
+}  // namespace dsa

@@ -1,0 +1,129 @@
+// sparse_attn.hip -- threshold-driven sparse attention (gfx950).
+//
+// Replaces _sparse_attn_kernel + sparse_attention_with_threshold_triton
+// (reference dsa_attention.py:234-324) and is the last stage of the split
+// forward and of the precomputed-threshold path (dsa_hybrid.py:66).  The
+// reference loads every K/V row of the prefix and masks; this kernel reads
+// only the score row and the selected K/V rows (attn_tile.h).
+//
+// Block = 4 waves = 4 consecutive queries of one batch element.  Blocks are
+// ordered longest query first within each batch element, and the batch
+// elements are spread over the XCDs in contiguous ranges so the K/V rows a
+// batch element gathers stay in one XCD's L2.
+#include "attn_tile.h"
+#include "dsa_launch.h"
+
+namespace dsa {
+namespace {
+
+struct AttnArgs {
+  const float* scores;
+  int64_t ld;
+  const float* thr;
+  const void* Q;
+  const void* K;
+  const void* V;
+  int64_t B;
+  int T;
+  int HQ, DQ, DV;
+  float scale_log2;
+  float* out;
+  int vec;
+};
+
+template <typename Tag, int EK, int EV>
+__global__ __launch_bounds__(256) void sparse_attn_kernel(AttnArgs a) {
+  using raw = typename Tag::raw;
+  __shared__ int lists[4][kListCap];
+  const int wave = threadIdx.x >> 6;
+  const int T = a.T;
+  const int tiles = (T + 3) >> 2;
+  const uint32_t L = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int64_t b = L / tiles;
+  const int tile = tiles - 1 - static_cast<int>(L % tiles);
+  const int t = tile * 4 + wave;
+  if (t >= T) return;
+  const int64_t EQ = static_cast<int64_t>(a.HQ) * a.DQ;
+  const int64_t EVt = static_cast<int64_t>(a.HQ) * a.DV;
+  const raw* Q = static_cast<const raw*>(a.Q) + b * T * EQ;
+  const raw* K = static_cast<const raw*>(a.K) + b * T * EQ;
+  const raw* V = static_cast<const raw*>(a.V) + b * T * EVt;
+  const int64_t qrow = b * T + t;
+  const float* srow = a.scores + qrow * a.ld;
+  const float thr = a.thr[qrow];
+  const bool vec = a.vec != 0;
+  attend_query<Tag, EK, EV>(
+      Q, K, V, t, a.HQ, a.DQ, a.DV, a.scale_log2, thr,
+      [&](int s, float(&sv)[4]) {
+        if (vec) {
+          const float4 f = *reinterpret_cast<const float4*>(srow + s);
+          sv[0] = f.x; sv[1] = f.y; sv[2] = f.z; sv[3] = f.w;
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) sv[c] = (s + c <= t) ? srow[s + c] : 0.f;
+        }
+      },
+      lists[wave], a.out + qrow * EVt);
+}
+
+template <typename Tag, int EK, int EV>
+hipError_t launch(const AttnArgs& a, hipStream_t stream) {
+  const int64_t nblk = a.B * ((a.T + 3) / 4);
+  hipLaunchKernelGGL((sparse_attn_kernel<Tag, EK, EV>), dim3(static_cast<unsigned>(nblk)),
+                     dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+// (EK, EV) pairs with an instance: equal, or one a factor 2 from the other.
+#define DSA_ATTN_PAIRS(X, Tag) \
+  X(Tag, 1, 1) X(Tag, 1, 2) X(Tag, 2, 1) X(Tag, 2, 2) X(Tag, 2, 4) X(Tag, 4, 2) X(Tag, 4, 4) \
+  X(Tag, 4, 8) X(Tag, 8, 4) X(Tag, 8, 8) X(Tag, 8, 16) X(Tag, 16, 8) X(Tag, 16, 16)
+#define DSA_ATTN_PAIRS16(X, Tag) \
+  DSA_ATTN_PAIRS(X, Tag) X(Tag, 16, 32) X(Tag, 32, 16) X(Tag, 32, 32)
+
+#define DSA_ATTN_CASE(Tag, ek, ev) \
+  if (EK == ek && EV == ev) return launch<Tag, ek, ev>(a, stream);
+#define DSA_ATTN_HAS(Tag, ek, ev) \
+  if (EK == ek && EV == ev) return true;
+
+int elems_per_lane(int HQ, int D) {
+  const int e = HQ * D / kWave;
+  return e < 1 ? 1 : e;
+}
+
+bool pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+}  // namespace
+
+bool sparse_attn_supported(int dtype, int HQ, int DQ, int DV) {
+  if (!pow2(HQ) || !pow2(DQ) || !pow2(DV)) return false;
+  const int EK = elems_per_lane(HQ, DQ), EV = elems_per_lane(HQ, DV);
+  if (EK > DQ || EV > DV) return false;  // a lane's slice must stay inside one head
+  if (dtype == 0) {
+    DSA_ATTN_PAIRS(DSA_ATTN_HAS, F32)
+  } else if (dtype == 1 || dtype == 2) {
+    DSA_ATTN_PAIRS16(DSA_ATTN_HAS, BF16)
+  }
+  return false;
+}
+
+hipError_t launch_sparse_attn(const float* scores, int64_t ld, const float* thr, const void* Q,
+                              const void* K, const void* V, int dtype, int64_t B, int64_t T,
+                              int HQ, int DQ, int DV, float scale, float* out,
+                              hipStream_t stream) {
+  if (B == 0 || T == 0) return hipSuccess;
+  const bool vec = (ld % 4 == 0) && ((reinterpret_cast<uintptr_t>(scores) & 15u) == 0);
+  AttnArgs a{scores, ld, thr, Q, K, V, B, static_cast<int>(T), HQ, DQ, DV,
+             scale * 1.4426950408889634f, out, vec ? 1 : 0};
+  const int EK = elems_per_lane(HQ, DQ), EV = elems_per_lane(HQ, DV);
+  if (dtype == 0) {
+    DSA_ATTN_PAIRS(DSA_ATTN_CASE, F32)
+  } else if (dtype == 1) {
+    DSA_ATTN_PAIRS16(DSA_ATTN_CASE, BF16)
+  } else if (dtype == 2) {
+    DSA_ATTN_PAIRS16(DSA_ATTN_CASE, F16)
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace dsa

@@ -1,0 +1,113 @@
+"""DeepSeek-V3.2 lightning indexer on MI355X -- drop-in for the reference's
+lightning_indexer.py (same names, arguments, return shapes and error classes).
+
+    I[b,t,s] = sum_j w[b,t,j] * ReLU(<q[b,t,j,:], k[b,s,:]>)   for s <= t, -inf otherwise
+
+    h   [B,T,D]   W_Q [D,H*d]   W_K [D,d]   W_W [D,H]   ->  scores [B,T,T] fp32
+
+`indexer_scores_triton` / `indexer_triton` keep the reference's names so
+callers switch without edits; they run the gfx950 MFMA kernel in
+libdsa_amd.so (no Triton).  `indexer_scores_torch`, `project`,
+`indexer_torch` are the reference's plain-torch functions, kept as API.
+"""
+from __future__ import annotations
+
+import torch
+
+import _dsa_lib as L
+
+
+# ---------------------------------------------------------------------------
+# Plain-torch functions of the reference API (lightning_indexer.py:26-47)
+# ---------------------------------------------------------------------------
+def indexer_scores_torch(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """q: [B,T,H,d]  k: [B,T,d]  w: [B,T,H] -> scores [B,T,T] (reference :26-33)."""
+    B, T, H, d = q.shape
+    dots = torch.einsum("bthd,bsd->bths", q, k)
+    scores = (w.unsqueeze(-1) * torch.relu(dots)).sum(dim=2)
+    causal = torch.ones(T, T, device=q.device, dtype=torch.bool).tril()
+    return scores.masked_fill(~causal, float("-inf"))
+
+
+def project(h: torch.Tensor, W_Q: torch.Tensor, W_K: torch.Tensor, W_W: torch.Tensor,
+            num_heads: int, head_dim: int):
+    """h@W projections to (q [B,T,H,d], k [B,T,d], w [B,T,H]) (reference :36-42)."""
+    B, T, _ = h.shape
+    q = (h @ W_Q).view(B, T, num_heads, head_dim)
+    k = h @ W_K
+    w = h @ W_W
+    return q, k, w
+
+
+def indexer_torch(h, W_Q, W_K, W_W, num_heads, head_dim):
+    q, k, w = project(h, W_Q, W_K, W_W, num_heads, head_dim)
+    return indexer_scores_torch(q, k, w)
+
+
+# ---------------------------------------------------------------------------
+# MI355X kernel (replaces _indexer_score_kernel + indexer_scores_triton, :54-125)
+# ---------------------------------------------------------------------------
+def indexer_scores_hip(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor, *,
+                       write_upper: bool = True, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Indexer scores [B,T,T] fp32 from the gfx950 MFMA kernel.
+
+    write_upper=False leaves the s > t triangle untouched (the split pipeline
+    never reads it).  `out` may be a preallocated [B,T,T] fp32 buffer.
+    """
+    L.require_gpu(q, k, w)
+    B, T, H, d = q.shape
+    assert k.shape == (B, T, d), f"k shape {tuple(k.shape)} != {(B, T, d)}"
+    assert w.shape == (B, T, H), f"w shape {tuple(w.shape)} != {(B, T, H)}"
+    dt = L.common_dtype(q, k, w)
+    q, k, w = (L.prep(x, dt) for x in (q, k, w))
+    if out is None:
+        out = torch.empty((B, T, T), device=q.device, dtype=torch.float32)
+    else:
+        assert out.shape == (B, T, T) and out.dtype == torch.float32 and out.is_contiguous()
+    rc = L.lib().dsa_indexer_scores(q.data_ptr(), k.data_ptr(), w.data_ptr(), L.dtype_code(dt),
+                                    B, T, H, d, out.data_ptr(), T, 1 if write_upper else 0,
+                                    L.stream_ptr(q.device))
+    L.check(rc, "indexer_scores")
+    return out
+
+
+def indexer_scores_triton(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor,
+                          BLOCK_T: int = 64, BLOCK_S: int = 64) -> torch.Tensor:
+    """Drop-in for the reference's indexer_scores_triton (:100-125).
+
+    Same checks (GPU tensors, shapes, power-of-two head_dim) and output:
+    fp32 [B,T,T], causal scores, -inf above the diagonal.  BLOCK_T/BLOCK_S
+    are accepted for compatibility; the gfx950 kernel picks its own tiles.
+    """
+    assert q.is_cuda and k.is_cuda and w.is_cuda
+    B, T, H, d = q.shape
+    assert k.shape == (B, T, d)
+    assert w.shape == (B, T, H)
+    assert d > 0 and d & (d - 1) == 0, f"head_dim {d} must be power of 2"
+    return indexer_scores_hip(q, k, w, write_upper=True)
+
+
+def indexer_triton(h, W_Q, W_K, W_W, num_heads, head_dim, **kw):
+    """Projection (hipBLASLt GEMMs via torch) then the MFMA indexer (:128-130)."""
+    q, k, w = project(h, W_Q, W_K, W_W, num_heads, head_dim)
+    return indexer_scores_triton(q, k, w, **kw)
+
+
+# ---------------------------------------------------------------------------
+# Top-k mask helper (reference :137-144)
+# ---------------------------------------------------------------------------
+def topk_mask(scores: torch.Tensor, k: int) -> torch.Tensor:
+    """Boolean [B,T,T] mask of the top-k key positions of every query row.
+
+    Built from the radix-select's exactly-k index set: the lowest index wins
+    ties, so the mask is deterministic (the reference took torch.topk's
+    indices, whose tie order is unspecified).  GPU tensors only.
+    """
+    from topk_threshold import topk_indices
+
+    L.require_gpu(scores)
+    B, T, _ = scores.shape
+    _, idx = topk_indices(scores, min(k, T))
+    mask = torch.zeros_like(scores, dtype=torch.bool)
+    mask.scatter_(-1, idx.long(), True)
+    return mask

@@ -1,0 +1,85 @@
+"""GPU k-th-largest ("top-K threshold") -- drop-in for the reference's CPU
+extension API (topk_avx512.cpp:226-264: topk_threshold and
+topk_threshold_batch_merge), re-hosted on the MI355X radix-select.
+
+Same contract: scores fp32, contiguous, k > 0, k <= N; returns the k-th
+largest of each row of the last dimension (ties counted) as a tensor of
+shape sizes[:-1] + [1] -- bit-identical to torch.topk(x, k).values[..., -1:].
+Same error class: RuntimeError (the extension's TORCH_CHECK).  The only
+difference is where the tensor lives: here it must be on the GPU (the
+reference's must be on the CPU).
+
+Extras the reference lacks: `topk_indices` (the exactly-k index set, lowest
+index winning ties) and a `causal` mode for [B,T,T] indexer matrices that
+reads only the s <= t entries of each row.
+"""
+from __future__ import annotations
+
+import torch
+
+import _dsa_lib as L
+
+
+def _check(scores: torch.Tensor, k: int) -> int:
+    if not scores.is_contiguous():
+        raise RuntimeError("scores must be contiguous")
+    if scores.dtype != torch.float32:
+        raise RuntimeError("fp32 only")
+    if not scores.is_cuda:
+        raise RuntimeError("GPU tensor required (MI355X radix-select)")
+    if k <= 0:
+        raise RuntimeError("k must be > 0")
+    if scores.dim() == 0:
+        raise RuntimeError("scores must have at least one dimension")
+    N = scores.shape[-1]
+    if k > N:
+        raise RuntimeError("k must be <= N")
+    return N
+
+
+def _select(scores: torch.Tensor, k: int, causal: bool, want_idx: bool):
+    N = _check(scores, k)
+    rows = scores.numel() // N if N else 0
+    causal_T = 0
+    if causal:
+        if scores.dim() < 2 or scores.shape[-2] != N:
+            raise RuntimeError("causal select needs [..., T, T] scores")
+        causal_T = N
+    thr = torch.empty(scores.shape[:-1] + (1,), device=scores.device, dtype=torch.float32)
+    idx = None
+    if want_idx:
+        idx = torch.empty(scores.shape[:-1] + (k,), device=scores.device, dtype=torch.int32)
+    if rows:
+        rc = L.lib().dsa_topk_threshold(scores.data_ptr(), rows, N, N, int(k), causal_T,
+                                        thr.data_ptr(), idx.data_ptr() if want_idx else None,
+                                        L.stream_ptr(scores.device))
+        if rc != L.DSA_OK:
+            msg = L.lib().dsa_last_error().decode(errors="replace")
+            raise RuntimeError(f"topk_threshold: {msg}")
+    return thr, idx
+
+
+def topk_threshold(scores: torch.Tensor, k: int, causal: bool = False) -> torch.Tensor:
+    """k-th largest of every row of the last dim -> shape [..., 1] fp32.
+
+    causal=True treats a [..., T, T] matrix as causal indexer scores: row t
+    reads only entries s <= t and counts the rest as -inf (what the
+    reference's masked full row holds), halving the bytes read.
+    """
+    return _select(scores, k, causal, False)[0]
+
+
+def topk_threshold_batch_merge(scores: torch.Tensor, k: int) -> torch.Tensor:
+    """The reference's batch-merge variant has the same contract and result
+    (topk_avx512.cpp:255-257); on the GPU there is one select kernel."""
+    return _select(scores, k, False, False)[0]
+
+
+def topk_indices(scores: torch.Tensor, k: int, causal: bool = False):
+    """(threshold [...,1] fp32, indices [...,k] int32).
+
+    indices = the k positions a stable descending sort puts first: every
+    entry above the threshold plus the lowest-index entries equal to it, in
+    ascending index order.
+    """
+    return _select(scores, k, causal, True)

@@ -1,0 +1,129 @@
+/*
+ * dsa_amd.h -- C ABI of the MI355X (gfx950) DeepSeek Sparse Attention forward.
+ *
+ * One shared library, libdsa_amd.so, built with hipcc for gfx950 only.  Every
+ * entry point:
+ *   - takes plain device pointers, sizes and a hipStream_t passed as void*
+ *     (NULL = the legacy default stream);
+ *   - enqueues its kernels on that stream and returns without synchronising;
+ *   - never allocates, frees or synchronises device memory;
+ *   - returns DSA_OK (0), a negative code for an argument the caller got wrong
+ *     (the Python layer raises AssertionError, as the reference's asserts do),
+ *     or a positive code for a HIP runtime failure (RuntimeError);
+ *   - records a message for any non-zero return, read back with
+ *     dsa_last_error() on the same thread.
+ * Arguments are validated before any HIP call, so a wrong argument is reported
+ * without touching a GPU.
+ *
+ * Layouts are dense row-major (C-contiguous), as the reference wrappers make
+ * them with .contiguous() before launching:
+ *   q_idx [B,T,HI,DI]   k_idx [B,T,DI]   w_idx [B,T,HI]        (dtype below)
+ *   Q,K   [B,T,HQ,DQ]   V     [B,T,HQ,DV]                     (dtype below)
+ *   scores [B,T,T] fp32 (row stride ld >= T)   thr [B*T] fp32   O [B,T,HQ,DV] fp32
+ */
+#ifndef DSA_AMD_H
+#define DSA_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type of q_idx/k_idx/w_idx and Q/K/V.  Arithmetic is fp32 in every
+ * case: 16-bit inputs feed MFMA with fp32 accumulation (products are exact),
+ * fp32 inputs use the fp32 MFMA.  Outputs are always fp32, as the reference's
+ * Triton wrappers allocate them (dsa_attention.py:210, :309). */
+enum dsa_dtype { DSA_F32 = 0, DSA_BF16 = 1, DSA_F16 = 2 };
+
+enum dsa_status {
+  DSA_OK = 0,
+  DSA_EINVAL = -1,       /* bad size, null pointer, k out of range, ...     */
+  DSA_EUNSUPPORTED = -2, /* a shape this build has no kernel for            */
+  DSA_EHIP = 1           /* a HIP runtime call failed (message says which)  */
+};
+
+/* Thread-local text of the last non-zero return on this thread. */
+const char* dsa_last_error(void);
+
+/* Library version string ("dsa_amd <semver> gfx950"). */
+const char* dsa_version(void);
+
+/*
+ * Lightning indexer scores.
+ *   scores[b,t,s] = sum_j w[b,t,j] * ReLU(<q[b,t,j,:], k[b,s,:]>)   for s <= t
+ *   scores[b,t,s] = -inf                                              for s >  t
+ * The upper triangle (s > t) is written only when write_upper != 0; the
+ * internal split pipeline skips it because nothing reads it.
+ * Replaces: _indexer_score_kernel + indexer_scores_triton,
+ *           reference lightning_indexer.py:54-125 (torch form :26-33).
+ * Constraints: B,T >= 1; 1 <= HI <= 256; DI in {16,32,64,128,256} (fp32) or
+ *              {32,64,128,256} (bf16/fp16); ld >= T.
+ */
+int dsa_indexer_scores(const void* q_idx, const void* k_idx, const void* w_idx,
+                       int dtype, int64_t B, int64_t T, int HI, int DI,
+                       float* scores, int64_t ld, int write_upper,
+                       void* stream);
+
+/*
+ * Per-row k-th largest ("top-K threshold") with an optional exactly-k index set.
+ *   thr[r] = k-th largest of row r, ties counted (torch.topk(x,k).values[...,-1]).
+ *   idx[r*k .. r*k+k) (optional, may be NULL) = the k positions a stable
+ *   descending sort of row r puts first -- every entry above thr[r] plus the
+ *   lowest-index entries equal to thr[r] -- written in ascending index order.
+ * causal_T == 0: every row has n valid entries.
+ * causal_T  > 0: row r is query t = r % causal_T of a [B,T,T] score matrix;
+ *   only its first t+1 entries are read and the rest count as -inf, exactly as
+ *   the reference's masked full row (dsa_attention.py:41-44): rows with
+ *   t+1 < k get thr = -inf.
+ * -0.0 and +0.0 compare equal; NaN ranks above +inf (as in torch.topk).
+ * Replaces: topk_threshold / topk_threshold_batch_merge, reference
+ *   topk_avx512.cpp:226-264, and scores.topk(...)[..., -1:] at
+ *   dsa_attention.py:343-344 (and the in-kernel tl.sort at :151-155).
+ * Constraints: rows >= 0; 1 <= k <= n; ld >= n; n < 2^31.
+ */
+int dsa_topk_threshold(const float* scores, int64_t rows, int64_t n, int64_t ld,
+                       int k, int64_t causal_T, float* thr, int32_t* idx,
+                       void* stream);
+
+/*
+ * Sparse attention restricted to keys whose indexer score passes a threshold.
+ *   sel(b,t,s) = (s <= t) && (scores[b,t,s] >= thr[b*T+t])   (ties kept)
+ *   O[b,t,h,:] = sum_{s in sel} softmax_s(<Q[b,t,h],K[b,s,h]> * scale) V[b,s,h,:]
+ * Rows that select nothing (only possible for a NaN or +inf threshold) get
+ * O = 0.  The threshold may come from anywhere (the reference's hybrid path
+ * computes it on the CPU, dsa_hybrid.py:61-66).
+ * Replaces: _sparse_attn_kernel + sparse_attention_with_threshold_triton,
+ *           reference dsa_attention.py:234-324.
+ * Constraints: HQ*DQ and HQ*DV powers of two with DQ, DV >= 1 powers of two,
+ *   HQ*DQ <= 64*32 and HQ*DV <= 64*32 (fp32: 64*8); ld >= T.
+ */
+int dsa_sparse_attn_threshold(const float* scores, int64_t ld, const float* thr,
+                              const void* Q, const void* K, const void* V,
+                              int dtype, int64_t B, int64_t T, int HQ, int DQ,
+                              int DV, float scale, float* out, void* stream);
+
+/*
+ * Fused DSA forward for T <= 2048: indexer -> per-row radix select ->
+ * sparse attention in one kernel; the score rows live in LDS only.
+ * Same result as dsa_indexer_scores + dsa_topk_threshold(k = min(top_k,T),
+ * causal) + dsa_sparse_attn_threshold.
+ * Replaces: _dsa_fused_kernel + dsa_attention_triton,
+ *           reference dsa_attention.py:96-227.
+ * Constraints: 1 <= T <= 2048; 1 <= top_k; the indexer's and the sparse
+ *   attention's head/dim constraints.
+ */
+int dsa_fused_forward(const void* q_idx, const void* k_idx, const void* w_idx,
+                      const void* Q, const void* K, const void* V, int dtype,
+                      int64_t B, int64_t T, int HI, int DI, int HQ, int DQ,
+                      int DV, int top_k, float scale, float* out, void* stream);
+
+/* Largest T dsa_fused_forward accepts (2048). */
+int64_t dsa_fused_max_T(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSA_AMD_H */

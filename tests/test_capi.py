@@ -1,0 +1,172 @@
+"""CPU: the C-ABI library loads, exports every symbol include/dsa_amd.h
+declares, and rejects bad arguments before touching a GPU; the Python layer
+keeps the reference's error classes.  No kernel is launched here."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import _dsa_lib as L
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dsa_amd.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dsa_[A-Za-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = L.lib()
+    names = declared_functions()
+    assert len(names) >= 7, names
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in dsa_amd.h but not exported"
+
+
+def test_export_list_matches_header():
+    """Every exported dsa_* function is declared in the header too."""
+    import subprocess
+
+    out = subprocess.run(["nm", "-D", "--defined-only", L.LIB_PATH], capture_output=True,
+                         text=True).stdout
+    exported = sorted({ln.split()[-1] for ln in out.splitlines() if " T dsa_" in ln})
+    assert exported == declared_functions()
+
+
+def test_version_and_limits():
+    lib = L.lib()
+    assert b"gfx950" in lib.dsa_version()
+    assert lib.dsa_fused_max_T() == 2048
+
+
+def _rc(fn, *args):
+    rc = fn(*args)
+    return rc, L.lib().dsa_last_error().decode()
+
+
+FAKE = 0x1000  # never dereferenced: validation fails first
+
+
+def test_topk_rejects_bad_arguments():
+    f = L.lib().dsa_topk_threshold
+    cases = [
+        ((FAKE, 4, 16, 16, 0, 0, FAKE, None, None), "k must be > 0"),
+        ((FAKE, 4, 16, 16, 17, 0, FAKE, None, None), "k must be <= N"),
+        ((FAKE, 4, 16, 8, 2, 0, FAKE, None, None), "ld"),
+        ((FAKE, -1, 16, 16, 2, 0, FAKE, None, None), "negative"),
+        ((FAKE, 6, 16, 16, 2, 4, FAKE, None, None), "multiple"),
+        ((FAKE, 4, 16, 16, 2, 32, FAKE, None, None), "causal_T"),
+        ((None, 4, 16, 16, 2, 0, FAKE, None, None), "null"),
+        ((FAKE, 1, 1 << 31, 1 << 31, 2, 0, FAKE, None, None), "2^31"),
+    ]
+    for args, needle in cases:
+        rc, msg = _rc(f, *args)
+        assert rc == L.DSA_EINVAL, (args, rc, msg)
+        assert needle in msg, (needle, msg)
+    # zero rows is a no-op, not an error
+    assert f(None, 0, 16, 16, 2, 0, None, None, None) == L.DSA_OK
+
+
+def test_indexer_rejects_bad_arguments():
+    f = L.lib().dsa_indexer_scores
+    ok = (FAKE, FAKE, FAKE, L.DSA_F32, 2, 64, 4, 32, FAKE, 64, 1, None)
+    assert _rc(f, *ok[:4], 2, 64, 4, 32, FAKE, 32, 1, None)[0] == L.DSA_EINVAL       # ld < T
+    assert _rc(f, *ok[:3], 7, *ok[4:])[0] == L.DSA_EINVAL                              # dtype
+    assert _rc(f, *ok[:6], 0, *ok[7:])[0] == L.DSA_EINVAL                              # HI
+    assert _rc(f, *ok[:7], 24, *ok[8:])[0] == L.DSA_EUNSUPPORTED                       # DI
+    assert _rc(f, FAKE, FAKE, FAKE, L.DSA_BF16, 2, 64, 4, 16, FAKE, 64, 1, None)[0] == L.DSA_EUNSUPPORTED
+    assert _rc(f, FAKE + 4, *ok[1:])[0] == L.DSA_EINVAL                                # alignment
+    assert _rc(f, None, *ok[1:])[0] == L.DSA_EINVAL                                    # null
+    assert f(*ok[:4], 0, *ok[5:]) == L.DSA_OK                                          # B = 0
+
+
+def test_sparse_attn_rejects_bad_arguments():
+    f = L.lib().dsa_sparse_attn_threshold
+    base = [FAKE, 64, FAKE, FAKE, FAKE, FAKE, L.DSA_F32, 2, 64, 4, 32, 32, 0.17, FAKE, None]
+
+    def call(**kw):
+        a = list(base)
+        for i, v in kw.items():
+            a[int(i[1:])] = v
+        return _rc(f, *a)
+
+    assert call(a9=3)[0] == L.DSA_EINVAL                 # HQ not a power of 2
+    assert call(a10=24)[0] == L.DSA_EINVAL               # DQ not a power of 2
+    assert call(a1=32)[0] == L.DSA_EINVAL                # ld < T
+    assert call(a12=float("nan"))[0] == L.DSA_EINVAL     # scale
+    assert call(a0=None)[0] == L.DSA_EINVAL              # null scores
+    assert call(a9=128, a10=1, a11=1)[0] == L.DSA_EUNSUPPORTED   # HQ > 64 lanes per head
+    assert call(a7=0)[0] == L.DSA_OK
+
+
+def test_fused_rejects_bad_arguments():
+    f = L.lib().dsa_fused_forward
+    base = [FAKE] * 6 + [L.DSA_F32, 2, 64, 4, 32, 4, 32, 32, 8, 0.17, FAKE, None]
+    a = list(base); a[8] = 4096
+    assert _rc(f, *a)[0] == L.DSA_EUNSUPPORTED           # T above the fused limit
+    a = list(base); a[14] = 0
+    assert _rc(f, *a)[0] == L.DSA_EINVAL                 # top_k < 1
+    a = list(base); a[10] = 24
+    assert _rc(f, *a)[0] == L.DSA_EUNSUPPORTED           # DI
+
+
+def test_status_mapping():
+    with pytest.raises(AssertionError):
+        L.check(L.DSA_EINVAL, "x")
+    with pytest.raises(L.DSAUnsupported):
+        L.check(L.DSA_EUNSUPPORTED, "x")
+    with pytest.raises(RuntimeError):
+        L.check(L.DSA_EHIP, "x")
+
+
+# ---------------------------------------------------------------------------
+# Python drop-ins keep the reference's checks and error classes (CPU tensors:
+# they must fail before any kernel launch).
+# ---------------------------------------------------------------------------
+def test_topk_threshold_contract_errors():
+    from topk_threshold import topk_threshold
+
+    x = torch.randn(4, 16)
+    with pytest.raises(RuntimeError, match="contiguous"):
+        topk_threshold(x.t(), 2)
+    with pytest.raises(RuntimeError, match="fp32"):
+        topk_threshold(x.double(), 2)
+    with pytest.raises(RuntimeError, match="GPU"):
+        topk_threshold(x, 2)
+
+
+def test_dsa_asserts_match_reference():
+    import dsa_attention as D
+
+    def mk(T=32, HI=4, DI=32, HQ=4, D_=32):
+        return (torch.zeros(1, T, HI, DI), torch.zeros(1, T, DI), torch.zeros(1, T, HI),
+                torch.zeros(1, T, HQ, D_), torch.zeros(1, T, HQ, D_), torch.zeros(1, T, HQ, D_))
+
+    with pytest.raises(AssertionError, match="power of 2"):
+        D.dsa_attention_triton(*mk(T=24), top_k=8, BLOCK_S=8)
+    with pytest.raises(AssertionError, match="power of 2"):
+        D.dsa_attention_triton(*mk(), top_k=6)
+    with pytest.raises(AssertionError, match="divisible"):
+        D.dsa_attention_triton(*mk(T=16), top_k=8, BLOCK_S=32)
+    with pytest.raises(AssertionError):
+        D.dsa_attention_split_triton(*mk(), top_k=64)
+    with pytest.raises(AssertionError, match="power of 2"):
+        D.sparse_attention_with_threshold_triton(torch.zeros(1, 24, 24), torch.zeros(1, 24, 1),
+                                                 *mk(T=24)[3:])
+    # valid shapes on CPU tensors: rejected as non-GPU input, no launch
+    with pytest.raises(AssertionError, match="GPU"):
+        D.dsa_attention_triton(*mk(), top_k=8)
+
+
+def test_indexer_asserts_match_reference():
+    from lightning_indexer import indexer_scores_triton
+
+    with pytest.raises(AssertionError):
+        indexer_scores_triton(torch.zeros(1, 8, 2, 16), torch.zeros(1, 8, 16), torch.zeros(1, 8, 2))

@@ -1,0 +1,106 @@
+"""GPU: threshold-driven sparse attention vs the float64 oracle on the same
+score matrix and threshold (rtol/atol 1e-4 fp32, 2e-2 16-bit)."""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from dsa_attention import sparse_attention_hip, sparse_attention_with_threshold_triton
+from helpers import close, say
+from oracle import dsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def run_case(dev, B, T, HQ, DQ, DV, thr_fn, dtype=torch.float32, rtol=1e-4, atol=1e-4,
+             seed0=0, rows=None):
+    say(f"attn B={B} T={T} HQ={HQ} DQ={DQ} DV={DV} {dtype}")
+    _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, HQ, DQ, DV, dtype=dtype, seed0=seed0)
+    g = torch.Generator().manual_seed(seed0 + 17)
+    scores = torch.randn(B, T, T, generator=g)
+    scores = torch.where(torch.rand(B, T, T, generator=g) < 0.1, 0.0, scores)   # ties at 0
+    thr = thr_fn(scores)
+    out = sparse_attention_hip(scores.to(dev), thr.to(dev), Q.to(dev), K.to(dev), V.to(dev))
+    torch.cuda.synchronize()
+    if rows is None:
+        want = O.sparse_attn_threshold(scores, thr, Q, K, V)
+        got = out.cpu()
+    else:
+        want = O.sparse_attn_threshold(scores[:, rows], thr[:, rows], Q, K, V, rows=rows)
+        got = out[:, rows].cpu()
+    ok, err, _ = close(got, want, rtol, atol)
+    assert ok, f"max abs err {err}"
+    return out
+
+
+def kth(k):
+    def f(scores):
+        T = scores.shape[-1]
+        masked = scores.masked_fill(~torch.ones(T, T, dtype=torch.bool).tril(), -math.inf)
+        return O.topk_threshold(masked, min(k, T))
+    return f
+
+
+@pytest.mark.parametrize("B,T,HQ,D,k", [(1, 128, 4, 32, 8), (16, 512, 4, 32, 32),
+                                        (2, 32, 2, 16, 8), (2, 300, 8, 64, 40),
+                                        (1, 257, 1, 64, 16), (1, 64, 64, 1, 8),
+                                        (2, 200, 16, 64, 20)])
+def test_kth_threshold(dev, B, T, HQ, D, k):
+    run_case(dev, B, T, HQ, D, D, kth(k))
+
+
+@pytest.mark.parametrize("HQ,DQ,DV", [(4, 32, 64), (4, 64, 32), (2, 16, 32), (8, 64, 128)])
+def test_dq_ne_dv(dev, HQ, DQ, DV):
+    run_case(dev, 2, 160, HQ, DQ, DV, kth(12))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("HQ,D", [(16, 128), (4, 32), (8, 64)])
+def test_16bit(dev, dtype, HQ, D):
+    run_case(dev, 2, 256, HQ, D, D, kth(24), dtype=dtype, rtol=2e-2, atol=2e-2)
+
+
+def test_external_thresholds(dev):
+    """Any threshold tensor works (the hybrid path's CPU-made threshold)."""
+    # -inf: every causal key -> dense causal attention
+    run_case(dev, 2, 200, 4, 32, 32, lambda s: torch.full(s.shape[:2] + (1,), -math.inf))
+    # random thresholds, capped at the s = t score so every row keeps a key
+    run_case(dev, 2, 200, 4, 32, 32,
+             lambda s: torch.minimum(torch.randn(s.shape[:2] + (1,),
+                                                 generator=torch.Generator().manual_seed(3)),
+                                     s.diagonal(0, 1, 2)[..., None]))
+    # threshold = the score at s = t: keeps exactly the keys scoring >= the diagonal one
+    run_case(dev, 2, 200, 4, 32, 32, lambda s: s.diagonal(0, 1, 2)[..., None].contiguous())
+
+
+def test_single_key_gives_v_row(dev):
+    B, T, HQ, D = 1, 96, 4, 32
+    _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, HQ, D, D)
+    scores = torch.zeros(B, T, T)
+    star = torch.randint(0, 10 ** 6, (T,), generator=torch.Generator().manual_seed(1)) % \
+        (torch.arange(T) + 1)
+    scores[0, torch.arange(T), star] = 1.0
+    out = sparse_attention_hip(scores.to(dev), torch.ones(B, T, 1, device=dev), Q.to(dev),
+                               K.to(dev), V.to(dev)).cpu()
+    assert torch.allclose(out[0], V[0, star], rtol=1e-6, atol=1e-6)
+
+
+def test_c4_shape_sampled_rows(dev):
+    rows = [0, 100, 2047, 2048, 4000, 16383]
+    run_case(dev, 1, 16384, 16, 128, 128, kth(2048), dtype=torch.bfloat16, rtol=2e-2,
+             atol=2e-2, rows=rows)
+
+
+def test_reference_wrapper_asserts_and_strided_threshold(dev):
+    """threshold may be a non-contiguous view, e.g. topv[..., -1:] (:343-344)."""
+    B, T = 2, 64
+    _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, 4, 32, 32)
+    s = torch.randn(B, T, T)
+    s = s.masked_fill(~torch.ones(T, T, dtype=torch.bool).tril(), -math.inf)
+    topv = torch.topk(s, 8, dim=-1).values
+    out = sparse_attention_with_threshold_triton(s.to(dev), topv.to(dev)[..., -1:], Q.to(dev),
+                                                 K.to(dev), V.to(dev)).cpu()
+    want = O.sparse_attn_threshold(s, topv[..., -1:], Q, K, V)
+    assert close(out, want, 1e-4, 1e-4)[0]

@@ -1,0 +1,110 @@
+"""GPU: MFMA lightning-indexer parity vs the float64 oracle (rtol/atol 1e-4
+for fp32 inputs, 2e-2 for 16-bit inputs; off-causal entries exactly -inf)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from helpers import close, say
+from lightning_indexer import indexer_scores_hip, indexer_scores_triton, indexer_triton
+from oracle import dsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def run_case(dev, B, T, HI, DI, dtype=torch.float32, rtol=1e-4, atol=1e-4, seed0=0,
+             rows=None, w_scale=None, scale=1.0):
+    say(f"indexer B={B} T={T} HI={HI} DI={DI} {dtype}")
+    q, k, w, *_ = O.make_inputs(B, T, HI, DI, 1, 1, 1, dtype=dtype, seed0=seed0,
+                                w_scale=w_scale, scale=scale)
+    s = indexer_scores_triton(q.to(dev), k.to(dev), w.to(dev)) if rows is None else \
+        indexer_scores_hip(q.to(dev), k.to(dev), w.to(dev))
+    torch.cuda.synchronize()
+    got = s.cpu() if rows is None else s[:, rows].cpu()
+    want = O.indexer_scores(q, k, w, rows=rows)
+    ts = torch.arange(T) if rows is None else torch.tensor(rows)
+    causal = torch.arange(T)[None, :] <= ts[:, None]
+    ok, err, _ = close(got[:, causal], want[:, causal], rtol, atol)
+    assert ok, f"max abs err {err}"
+    assert bool(torch.isneginf(got[:, ~causal]).all()), "off-causal entries must be -inf"
+    return s
+
+
+@pytest.mark.parametrize("B,T,H,d", [(1, 64, 4, 64), (2, 128, 8, 64), (1, 200, 4, 32)])
+def test_reference_shapes(dev, B, T, H, d):
+    """test_indexer.py:18-33 (N(0,1) inputs, atol = rtol = 1e-4)."""
+    run_case(dev, B, T, H, d, w_scale=1.0)
+
+
+@pytest.mark.parametrize("B,T,HI,DI", [(1, 128, 4, 32), (16, 512, 4, 32), (2, 37, 3, 16),
+                                       (3, 100, 2, 16), (1, 300, 5, 128), (1, 96, 9, 256),
+                                       (2, 1024, 8, 64)])
+def test_shapes_fp32(dev, B, T, HI, DI):
+    run_case(dev, B, T, HI, DI)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,T,HI,DI", [(1, 256, 64, 128), (2, 130, 4, 32), (1, 200, 12, 64),
+                                       (1, 64, 8, 256)])
+def test_shapes_16bit(dev, dtype, B, T, HI, DI):
+    # products of 16-bit inputs are exact in fp32 and the sum is fp32, so the
+    # error is fp32 rounding only; 2e-2 is the north-star bound.
+    run_case(dev, B, T, HI, DI, dtype=dtype, rtol=2e-2, atol=2e-2)
+
+
+def test_c3_shape_sampled_rows(dev):
+    T = 4096
+    rows = [0, 1, 15, 16, 255, 256, 1000, 2047, 4094, 4095]
+    run_case(dev, 4, T, 8, 64, rows=rows)
+
+
+def test_c4_shape_sampled_rows(dev):
+    T = 16384
+    rows = [0, 5, 2047, 2048, 9000, 16383]
+    run_case(dev, 1, T, 64, 128, dtype=torch.bfloat16, rtol=2e-2, atol=2e-2, rows=rows)
+
+
+def test_write_upper_false_leaves_upper_untouched(dev):
+    q, k, w, *_ = O.make_inputs(2, 200, 4, 32, 1, 1, 1)
+    out = torch.full((2, 200, 200), 123.0, device=dev)
+    indexer_scores_hip(q.to(dev), k.to(dev), w.to(dev), write_upper=False, out=out)
+    upper = torch.ones(200, 200, dtype=torch.bool, device=dev).triu(1)
+    assert bool((out[:, upper] == 123.0).all())
+    full = indexer_scores_hip(q.to(dev), k.to(dev), w.to(dev))
+    assert torch.equal(out[:, ~upper], full[:, ~upper])
+
+
+def test_projection_pipeline(dev):
+    """test_indexer.py:36-48: projection (torch GEMMs) + MFMA indexer, 1e-3."""
+    B, T, D, H, d = 2, 96, 128, 4, 64
+    g = torch.Generator().manual_seed(0)
+    h = torch.randn(B, T, D, generator=g)
+    W_Q = torch.randn(D, H * d, generator=g) * 0.1
+    W_K = torch.randn(D, d, generator=g) * 0.1
+    W_W = torch.randn(D, H, generator=g) * 0.1
+    out = indexer_triton(h.to(dev), W_Q.to(dev), W_K.to(dev), W_W.to(dev), H, d,
+                         BLOCK_T=32, BLOCK_S=32).cpu()
+    hq, hk, hw = (h.double() @ W.double() for W in (W_Q, W_K, W_W))
+    ref = O.indexer_scores(hq.view(B, T, H, d), hk, hw)
+    causal = torch.ones(T, T, dtype=torch.bool).tril()
+    assert float((out[:, causal].double() - ref[:, causal]).abs().max()) < 1e-3
+
+
+def test_topk_mask_consistency(dev):
+    """test_indexer.py:51-62: top-k masks from HIP scores and oracle scores
+    agree (>99%; near-tie flips allowed), and the HIP mask has exactly k
+    entries per row, the lowest indices winning ties."""
+    from lightning_indexer import topk_mask
+
+    B, T, H, d = 1, 64, 4, 64
+    q, k, w, *_ = O.make_inputs(B, T, H, d, 1, 1, 1, w_scale=1.0)
+    s = indexer_scores_triton(q.to(dev), k.to(dev), w.to(dev), BLOCK_T=32, BLOCK_S=32)
+    m = topk_mask(s, 8).cpu()
+    ref = O.indexer_scores(q, k, w)
+    mref = torch.zeros(B, T, T, dtype=torch.bool)
+    mref.scatter_(-1, torch.from_numpy(O.select_indices(ref.numpy(), 8)).long(), True)
+    assert float((m == mref).float().mean()) > 0.99
+    assert bool((m.sum(-1) == 8).all())
+    mine = torch.zeros(B, T, T, dtype=torch.bool)
+    mine.scatter_(-1, torch.from_numpy(O.select_indices(s.cpu().numpy(), 8)).long(), True)
+    assert torch.equal(m, mine)

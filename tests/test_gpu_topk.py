@@ -1,0 +1,154 @@
+"""GPU: radix-select parity.  Thresholds and exactly-k index sets must be
+bit-identical to the oracle on the same score matrix (north star: "top-K
+index set bit-exact when selection is run on the same score matrix, with ties
+broken by lowest index")."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import say
+from oracle import dsa_oracle as O
+from topk_threshold import topk_indices, topk_threshold, topk_threshold_batch_merge
+
+pytestmark = pytest.mark.gpu
+
+
+def cpu_randn(shape, seed):
+    return torch.randn(shape, generator=torch.Generator().manual_seed(seed), dtype=torch.float32)
+
+
+def check_rows(x_cpu, k, dev, causal=False, what=""):
+    say(f"topk {what} shape={tuple(x_cpu.shape)} k={k} causal={causal}")
+    thr, idx = topk_indices(x_cpu.to(dev), k, causal=causal)
+    torch.cuda.synchronize()
+    want_thr = O.topk_threshold(x_cpu, k)
+    assert torch.equal(thr.cpu(), want_thr), "threshold differs from torch.topk k-th value"
+    want_idx = O.select_indices(x_cpu.numpy(), k)
+    got_idx = idx.cpu().numpy()
+    bad = np.flatnonzero((got_idx != want_idx).any(-1).reshape(-1))
+    assert bad.size == 0, f"{bad.size} rows with a different index set, first row {bad[:3]}"
+    # threshold-only entry point agrees too
+    assert torch.equal(topk_threshold(x_cpu.to(dev), k, causal=causal).cpu(), want_thr)
+
+
+@pytest.mark.parametrize("rows,n,k", [
+    (8, 1, 1), (16, 5, 3), (33, 100, 7), (7, 256, 1), (5, 256, 256), (9, 513, 32),
+    (4, 1000, 999), (64, 2048, 128), (8, 4096, 256), (4, 8191, 100), (3, 16384, 2048),
+    (2, 32768, 5000), (2, 40000, 1234), (1, 100003, 77),
+])
+def test_random_rows(dev, rows, n, k):
+    check_rows(cpu_randn((rows, n), rows * 1000 + n), k, dev, what="randn")
+
+
+@pytest.mark.parametrize("n,k", [(64, 10), (512, 32), (2048, 128), (5000, 400), (40000, 3000)])
+def test_tie_heavy_rows(dev, n, k):
+    g = torch.Generator().manual_seed(n)
+    x = torch.randint(0, 6, (6, n), generator=g).float()
+    x[1] = 2.0                                           # one all-equal row
+    x[2] = torch.where(torch.rand(n, generator=g) < 0.5, 0.0, -0.0)   # +-0 only
+    x[3, : n // 2] = float("-inf")                       # half -inf
+    x[4] = float("-inf")                                 # all -inf
+    x[5, ::3] = float("inf")
+    check_rows(x, k, dev, what="ties")
+
+
+def test_special_values(dev):
+    x = cpu_randn((4, 300), 9)
+    x[0, 5] = float("inf")
+    x[1] = torch.finfo(torch.float32).max * torch.sign(x[1])
+    x[2] = torch.finfo(torch.float32).tiny * x[2]       # denormal-range magnitudes
+    x[3, :] = -0.0
+    for k in (1, 2, 150, 300):
+        check_rows(x, k, dev, what="special")
+
+
+def test_reference_extension_test_cases(dev):
+    """test_topk_avx512.py:20-35 on the GPU drop-in: torch.equal vs torch.topk."""
+    torch.manual_seed(0)
+    x = torch.randn(3, 128, 128, dtype=torch.float32)
+    for k in (1, 8, 16, 32, 64, 96, 128):
+        ref = x.topk(k, dim=-1).values[..., -1:]
+        assert torch.equal(topk_threshold(x.to(dev), k).cpu(), ref), f"k={k}"
+    torch.manual_seed(1)
+    x = torch.randn(3, 128, 128, dtype=torch.float32)
+    for k in (64, 128):
+        ref = x.topk(k, dim=-1).values[..., -1:]
+        assert torch.equal(topk_threshold_batch_merge(x.to(dev), k).cpu(), ref), f"k={k}"
+
+
+def test_golden_reference_vectors(dev):
+    """The reference's own compiled extension's outputs (tests/golden/ref_topk.npz)."""
+    import os
+
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "ref_topk.npz"))
+    for x, ks, thr in ((z["x0"], z["ks0"], z["thr0"]), (z["x1"], z["ks1"], z["thr1"])):
+        xg = torch.from_numpy(x).to(dev)
+        for i, k in enumerate(ks):
+            assert np.array_equal(topk_threshold(xg, int(k)).cpu().numpy(), thr[i]), f"k={k}"
+
+
+def test_standalone_c2_topk_vs_torch_topk_sets(dev):
+    """Config 2 standalone top-K: [64,2048,2048] N(0,1), k=128; thresholds
+    bit-exact and index sets equal to torch.topk's (tie-free data)."""
+    say("topk c2 standalone [64,2048,2048] k=128")
+    x = torch.randn((64, 2048, 2048), generator=torch.Generator().manual_seed(2),
+                    dtype=torch.float32)
+    xg = x.to(dev)
+    thr, idx = topk_indices(xg, 128)
+    tv, ti = torch.topk(xg, 128, dim=-1)
+    torch.cuda.synchronize()
+    assert torch.equal(thr, tv[..., -1:])
+    assert torch.equal(torch.sort(idx.long(), dim=-1).values, torch.sort(ti, dim=-1).values)
+    rows = [0, 77, 4095, 131071]
+    xr = x.reshape(-1, 2048)[rows]
+    assert np.array_equal(idx.reshape(-1, 128)[rows].cpu().numpy(), O.select_indices(xr.numpy(), 128))
+
+
+def test_causal_mode_on_indexer_scores(dev):
+    """Causal select on indexer score matrices: reads only s <= t; rows with
+    t+1 < k give -inf and indices 0..k-1."""
+    from lightning_indexer import indexer_scores_hip
+
+    for (B, T, HI, DI, k) in ((2, 512, 4, 32, 32), (2, 300, 4, 32, 64), (1, 2048, 8, 64, 256)):
+        q, kk, w, *_ = O.make_inputs(B, T, HI, DI, 1, 1, 1, seed0=T)
+        s = indexer_scores_hip(q.to(dev), kk.to(dev), w.to(dev), write_upper=True)
+        check_rows(s.cpu(), k, dev, causal=True, what=f"causal T={T}")
+        # garbage above the diagonal must not matter in causal mode
+        g = s.clone()
+        upper = torch.ones(T, T, dtype=torch.bool, device=dev).triu(1)
+        g[:, upper] = float("nan")
+        thr_c, idx_c = topk_indices(g, k, causal=True)
+        thr_f, idx_f = topk_indices(s, k, causal=False)
+        assert torch.equal(thr_c, thr_f) and torch.equal(idx_c, idx_f)
+
+
+def test_causal_c4_shape_properties(dev):
+    """Config-4 shape (T=16384, k=2048) at full size: size-independent
+    properties on every row, bit-exact on sampled rows."""
+    T, k = 16384, 2048
+    say("topk causal c4-shape T=16384 k=2048")
+    g = torch.Generator(device=dev).manual_seed(4)
+    s = torch.randn((1, T, T), generator=g, device=dev, dtype=torch.float32)
+    s = torch.where(torch.rand((1, T, T), generator=g, device=dev) < 0.05, 0.0, s)  # zero ties
+    thr, idx = topk_indices(s, k, causal=True)
+    torch.cuda.synchronize()
+    tril = torch.ones(T, T, dtype=torch.bool, device=dev).tril()
+    masked = s.masked_fill(~tril, float("-inf"))
+    n_gt = (masked > thr).sum(-1)[0]
+    n_ge = (masked >= thr).sum(-1)[0]
+    long_rows = torch.arange(T, device=dev) + 1 >= k
+    assert bool((n_gt[long_rows] < k).all()) and bool((n_ge[long_rows] >= k).all())
+    assert bool(torch.isneginf(thr[0, ~long_rows, 0]).all())
+    # every emitted index is a valid position whose score passes the threshold
+    vals = torch.gather(masked[0], 1, idx[0].long())
+    assert bool((vals >= thr[0]).all())
+    srt = torch.sort(idx[0].long(), dim=-1).values
+    assert bool((srt[:, 1:] > srt[:, :-1]).all()), "indices must be distinct and ascending"
+    del masked
+    rows = [0, 1, k - 2, k - 1, k, 5000, T - 2, T - 1]
+    sub = s[0, rows].cpu()
+    sub = sub.masked_fill(torch.arange(T)[None, :] > torch.tensor(rows)[:, None], float("-inf"))
+    assert torch.equal(thr[0, rows].cpu(), O.topk_threshold(sub, k))
+    assert np.array_equal(idx[0, rows].cpu().numpy(), O.select_indices(sub.numpy(), k))
