@@ -1,0 +1,301 @@
+"""Benchmark: DSA forward on one MI355X at BASELINE.json's headline config.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--mode graph|eager]
+
+Workload: B=16, T=512, k=32, HI=4, DI=32, HQ=4, DQ=DV=32, fp32,
+synthetic N(0,1) inputs (w ~ N(0,1)/sqrt(HI)) resident in HBM before timing.
+A step is one fused DSA forward (indexer -> radix-select -> sparse attention,
+one kernel).  Prints ONE JSON line:
+
+  value        query tokens/s over the K timed steps (B*T*K / seconds)
+  roofline     the fused kernel: algorithmic fp32 FLOPs per launch / its
+               average duration (HIP events around every launch on the stream
+               it runs on), against the fp32 MFMA peak (157.3 TFLOP/s)
+  topk_select  the radix-select at config 4's shape (T=16384, k=2048, causal
+               rows of real config-4 indexer scores): algorithmic bytes
+               4*sum(t+1) (+ outputs) / duration, against 8 TB/s
+  split        the split forward (indexer, select, attention) at config 1
+  cpu_baseline the reference's CPU path restated (oracle/, torch-vectorised
+               fp32 forward) on the host cores, plus the AVX-512 k-th-largest
+               (the reference's own topk_avx512.cpp from oracle/_ref when it
+               was built and the host has AVX-512, else this repo's port)
+
+--mode graph (default) replays the K steps from one HIP graph, so the Python
+launch path is out of the timed region; every kernel still runs every step.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "dsa-cpu-topk_amd")]
+
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, vendor figure
+PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix, vendor figure
+BASELINE_MS = 5.62             # reference fused Triton forward, README.md:49 (RTX PRO 6000)
+
+C1 = dict(B=16, T=512, k=32, HI=4, DI=32, HQ=4, DQ=32, DV=32)
+C4 = dict(B=1, T=16384, k=2048, HI=64, DI=128, HQ=16, DQ=128, DV=128)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def indexer_flops(B, T, HI, DI):
+    return B * T * (T + 1) / 2 * HI * (2 * DI + 2)
+
+
+def attention_flops(B, T, k, HQ, DQ, DV):
+    sel = sum(min(k, t + 1) for t in range(T))
+    return B * sel * HQ * (2 * DQ + 2 * DV)
+
+
+def gpu_inputs(cfg, dtype, dev, seed=0):
+    import torch
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    B, T, HI, DI, HQ, DQ, DV = (cfg[x] for x in ("B", "T", "HI", "DI", "HQ", "DQ", "DV"))
+
+    def rn(*shape, s=1.0):
+        return (torch.randn(shape, generator=g, device=dev, dtype=torch.float32) * s).to(dtype)
+
+    return (rn(B, T, HI, DI), rn(B, T, DI), rn(B, T, HI, s=1.0 / math.sqrt(HI)),
+            rn(B, T, HQ, DQ), rn(B, T, HQ, DQ), rn(B, T, HQ, DV))
+
+
+def time_events(fn, reps, stream):
+    """Mean duration (s) of fn() over reps, HIP events around each call."""
+    import torch
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(reps)]
+    for a, b in evs:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in evs) / reps / 1e3
+
+
+def bench_fused(args, dev):
+    import torch
+
+    import dsa_attention as D
+
+    ins = gpu_inputs(C1, torch.float32, dev)
+    k = C1["k"]
+    fwd = lambda: D.dsa_fused_hip(*ins, k)  # noqa: E731
+    for _ in range(args.warmup):
+        fwd()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+
+    # Per-launch HIP events: the kernel's average duration.
+    kern_s = time_events(fwd, max(20, min(args.steps, 200)), stream)
+
+    if args.mode == "graph":
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(args.steps):
+                fwd()
+        graph.replay()                 # warm the graph once (untimed)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        graph.replay()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    else:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            fwd()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    return elapsed, kern_s
+
+
+def bench_split(dev, reps=50):
+    import torch
+
+    import dsa_attention as D
+
+    ins = gpu_inputs(C1, torch.float32, dev, seed=1)
+    fwd = lambda: D.dsa_split_hip(*ins, C1["k"])  # noqa: E731
+    for _ in range(5):
+        fwd()
+    return time_events(fwd, reps, torch.cuda.current_stream(dev))
+
+
+def bench_select_c4(dev, reps=20):
+    """Radix-select on config-4 causal rows (real indexer scores)."""
+    import torch
+
+    from lightning_indexer import indexer_scores_hip
+    from topk_threshold import topk_indices, topk_threshold
+
+    T, k = C4["T"], C4["k"]
+    ins = gpu_inputs(C4, torch.bfloat16, dev, seed=4)
+    scores = indexer_scores_hip(*ins[:3], write_upper=False)
+    del ins
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(3):
+        topk_threshold(scores, k, causal=True)
+    t_thr = time_events(lambda: topk_threshold(scores, k, causal=True), reps, stream)
+    t_idx = time_events(lambda: topk_indices(scores, k, causal=True), reps, stream)
+    read = 4.0 * T * (T + 1) / 2
+    out_thr = 4.0 * T
+    out_idx = out_thr + 4.0 * T * k
+    res = {
+        "workload": "causal radix-select, config-4 indexer scores [1,16384,16384] fp32, k=2048",
+        "ms": round(t_thr * 1e3, 4),
+        "GB_per_s": round((read + out_thr) / t_thr / 1e9, 1),
+        "frac": round((read + out_thr) / t_thr / 1e9 / PEAK_HBM_GBS, 4),
+        "algorithmic_bytes": read + out_thr,
+        "with_indices_ms": round(t_idx * 1e3, 4),
+        "with_indices_GB_per_s": round((read + out_idx) / t_idx / 1e9, 1),
+        "peak_GB_per_s": PEAK_HBM_GBS,
+    }
+    del scores
+    # config-2 standalone top-K: [64,2048,2048] N(0,1), k=128
+    x = torch.randn((64, 2048, 2048), device=dev, dtype=torch.float32)
+    for _ in range(3):
+        topk_threshold(x, 128)
+    t2 = time_events(lambda: topk_threshold(x, 128), reps, stream)
+    b2 = 4.0 * x.numel() + 4.0 * 64 * 2048
+    res["c2_standalone"] = {"workload": "[64,2048,2048] N(0,1) fp32, k=128",
+                            "ms": round(t2 * 1e3, 4),
+                            "GB_per_s": round(b2 / t2 / 1e9, 1),
+                            "frac": round(b2 / t2 / 1e9 / PEAK_HBM_GBS, 4)}
+    return res
+
+
+def cpu_baseline(budget_s=12.0):
+    """The reference's CPU path, restated: torch-vectorised fp32 DSA forward
+    (oracle.dsa_forward, acc=float32) on config 1, plus the AVX-512
+    k-th-largest on config 1's score matrix."""
+    import numpy as np
+    import torch
+
+    from oracle import dsa_oracle as O
+    from oracle import native
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    os.environ.setdefault("OMP_NUM_THREADS", str(cores))
+    ins = O.make_inputs(C1["B"], C1["T"], C1["HI"], C1["DI"], C1["HQ"], C1["DQ"], C1["DV"])
+    k = C1["k"]
+    O.dsa_forward(*ins, k, acc=torch.float32)          # warm-up
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or n < 2:
+        O.dsa_forward(*ins, k, acc=torch.float32)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    tokens = C1["B"] * C1["T"]
+    res = {"value": round(tokens / dt, 1), "unit": "query tokens/s", "cores": cores,
+           "kind": "port",
+           "sample": f"config 1 (B=16,T=512,k=32) torch-vectorised fp32 forward x{n}, "
+                     f"{dt * 1e3:.1f} ms each",
+           "ms_per_step": round(dt * 1e3, 3), "cpu": native.cpu_model()}
+    # AVX-512 k-th largest on the config-1 score matrix [16,512,512], k=32
+    scores = O.indexer_scores(*ins[:3], acc=torch.float32).contiguous()
+    ref = native.ref()
+    if ref is not None:
+        fn = lambda: ref.topk_threshold(scores, k)  # noqa: E731
+        kind = "reference"
+    else:
+        s_np = scores.numpy()
+        fn = lambda: native.port_topk_threshold(s_np, k)  # noqa: E731
+        kind = "port"
+    for _ in range(5):
+        fn()
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 3.0 or reps < 30:
+        fn()
+        reps += 1
+    res["topk_avx512"] = {"kind": kind, "ms": round((time.perf_counter() - t0) / reps * 1e3, 4),
+                          "sample": "config-1 scores [16,512,512], k=32", "cores": cores,
+                          "avx512": "avx512f" in native.cpu_flags()}
+    return res
+
+
+def traffic_from_profile():
+    path = os.path.join(ROOT, "profiles", "fused_c1_traffic.json")
+    if os.path.exists(path):
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--mode", choices=("graph", "eager"), default="graph")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-select", action="store_true", help="skip the config-4 select leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build has no "
+              "multi-GPU path; see DESIGN.md for how the forward would shard.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    B, T = C1["B"], C1["T"]
+    log("bench: fused config 1")
+    elapsed, kern_s = bench_fused(args, dev)
+    ms = elapsed / args.steps * 1e3
+    value = B * T * args.steps / elapsed
+    flops = indexer_flops(B, T, C1["HI"], C1["DI"]) + attention_flops(
+        B, T, C1["k"], C1["HQ"], C1["DQ"], C1["DV"])
+    achieved = flops / kern_s / 1e12
+    log("bench: split config 1")
+    split_s = bench_split(dev)
+    out = {
+        "metric": "DSA fwd ms + query tokens/s at B=16,T=512,k=32; top-K HBM GB/s vs peak",
+        "value": round(value, 1),
+        "unit": "query tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(value / (B * T / (BASELINE_MS / 1e3)), 2),
+        "baseline": {"ms": BASELINE_MS, "source": "reference README.md:49, fused Triton on "
+                     "RTX PRO 6000 Blackwell"},
+        "dtype": "f32",
+        "data": "synthetic N(0,1) (w ~ N(0,1)/sqrt(HI)), resident in HBM",
+        "config": {"workload": "config 1: fused DSA forward (indexer + radix-select + sparse "
+                               "attention, one gfx950 kernel)",
+                   "B": B, "T": T, "top_k": C1["k"], "HI": C1["HI"], "DI": C1["DI"],
+                   "HQ": C1["HQ"], "DQ": C1["DQ"], "DV": C1["DV"], "mode": args.mode},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
+                     "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 5),
+                     "traffic": traffic_from_profile(),
+                     "kernel": "fused_kernel<F32,32,4,2,2>",
+                     "kernel_ms": round(kern_s * 1e3, 5),
+                     "flops_per_launch": flops},
+        "split": {"ms_per_step": round(split_s * 1e3, 5),
+                  "value": round(B * T / split_s, 1), "unit": "query tokens/s"},
+    }
+    if not args.no_select:
+        log("bench: select at config 4")
+        out["topk_select"] = bench_select_c4(dev)
+    if not args.no_cpu:
+        log("bench: CPU baseline")
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -61,7 +61,8 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerArgs a) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         const int s = s0 + 16 * kb + r16;
-        if (tq < T && s < c1) out[static_cast<int64_t>(tq) * a.ld + s] = (s <= tq) ? sc[kb] : ninf;
+        if (tq < T && s < c1 && (s <= tq || a.write_upper))
+          out[static_cast<int64_t>(tq) * a.ld + s] = (s <= tq) ? sc[kb] : ninf;
       }
     });
     const int span = s_end - c0;

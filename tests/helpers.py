@@ -46,13 +46,14 @@ def close(a, b, rtol, atol):
     return bool((err <= lim).all()), float(err.max()), float((err / lim).max())
 
 
-def flipped_rows(scores_a, scores_b, k):
+def flipped_rows(scores_a, scores_b, k, rows=None):
     """Rows whose selected set (>= k-th largest, ties kept) differs between
-    two score matrices [B,T,T] (CPU tensors)."""
+    two score matrices [B,R,T] (CPU tensors; R = T or len(rows))."""
     ta = O.topk_threshold(scores_a, k)
     tb = O.topk_threshold(scores_b, k)
     T = scores_a.shape[-1]
-    causal = torch.ones(T, T, dtype=torch.bool).tril()
+    ts = torch.arange(T) if rows is None else torch.as_tensor(rows)
+    causal = torch.arange(T)[None, :] <= ts[:, None]
     sa = (scores_a >= ta) & causal
     sb = (scores_b >= tb) & causal
     return (sa != sb).any(-1)          # [B,T] bool

@@ -104,7 +104,7 @@ def staged_check(dev, name, rows=None, rtol=1e-4, atol=1e-4, max_flip_frac=0.005
     # (3) from scratch, near-tie flips counted apart
     want0 = O.sparse_attn_threshold(s_ref, O.topk_threshold(s_ref, min(k, T)), *ins[3:],
                                     rows=rows)
-    flips = flipped_rows(s_cpu, s_ref, min(k, T))
+    flips = flipped_rows(s_cpu, s_ref, min(k, T), rows=rows)
     keep = ~flips
     ok, err, _ = close(split[:, sel].cpu()[keep], want0[keep], rtol, atol)
     assert ok, f"from-scratch max abs err {err}"
