@@ -125,7 +125,7 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
       cnt += keep[c] ? 1 : 0;
     }
     const int incl = wave_inclusive_sum(cnt);
-    const int total = __shfl(incl, kWave - 1, kWave);
+    const int total = wave_read_lane(incl, kWave - 1);
     int p = incl - cnt;
 #pragma unroll
     for (int c = 0; c < 4; ++c)

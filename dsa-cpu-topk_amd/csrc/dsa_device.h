@@ -37,10 +37,11 @@ __device__ __forceinline__ float to_f32(F16, uint16_t x) {
 // therefore free and marks "no element" (padding, masked positions).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t float_to_key(float f) {
+  f = f + 0.0f;  // IEEE: -0.0 + 0.0 = +0.0; every other value (and NaN-ness) unchanged
   uint32_t u = __float_as_uint(f);
-  u = (u == 0x80000000u) ? 0u : u;
-  u = ((u & 0x7fffffffu) > 0x7f800000u) ? 0x7fc00000u : u;
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  u = (f != f) ? 0x7fc00000u : u;
+  // negative: flip every bit; non-negative: set the sign bit
+  return u ^ (static_cast<uint32_t>(static_cast<int32_t>(u) >> 31) | 0x80000000u);
 }
 __device__ __forceinline__ float key_to_float(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
@@ -60,15 +61,35 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_wave_barrier();
 }
 
+// DPP lane move within the wave (no LDS traffic).  Lanes whose source falls
+// outside the pattern, or whose row is masked off, read 0.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Inclusive prefix sum over the 64 lanes (32-bit integer types): four
+// row_shr steps scan each 16-lane row, then row_bcast:15 and row_bcast:31
+// carry row totals into the rows above.
 template <typename T>
-__device__ __forceinline__ T wave_inclusive_sum(T v) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    T t = __shfl_up(v, o, kWave);
-    if (lane >= o) v += t;
-  }
-  return v;
+__device__ __forceinline__ T wave_inclusive_sum(T x) {
+  static_assert(sizeof(T) == 4, "32-bit lanes");
+  uint32_t v = static_cast<uint32_t>(x);
+  v += dpp_u32<0x111>(v);        // row_shr:1
+  v += dpp_u32<0x112>(v);        // row_shr:2
+  v += dpp_u32<0x114>(v);        // row_shr:4
+  v += dpp_u32<0x118>(v);        // row_shr:8
+  v += dpp_u32<0x142, 0xa>(v);   // row_bcast:15 into rows 1 and 3
+  v += dpp_u32<0x143, 0xc>(v);   // row_bcast:31 into rows 2 and 3
+  return static_cast<T>(v);
+}
+
+// Value of lane `src` (uniform) broadcast to the wave.
+template <typename T>
+__device__ __forceinline__ T wave_read_lane(T x, int src) {
+  static_assert(sizeof(T) == 4, "32-bit lanes");
+  return static_cast<T>(__builtin_amdgcn_readlane(static_cast<int>(x), src));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -93,8 +114,18 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
 }
 
+// Workgroup barrier that orders LDS traffic only.  __syncthreads() also
+// fences global memory, which makes every wave drain its outstanding global
+// loads at the barrier; kernels whose threads exchange data through LDS alone
+// use this one so that prefetched loads stay in flight across it.
+__device__ __forceinline__ void block_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Block-wide exclusive prefix sum in thread order (NT threads, NT % 64 == 0).
-// wsum must hold NT/64 words of LDS.  Contains two __syncthreads().
+// wsum must hold NT/64 words of LDS.  Contains two LDS-only barriers.
 template <int NT>
 __device__ __forceinline__ uint32_t block_exclusive_sum(uint32_t v, uint32_t* wsum,
                                                         uint32_t& total) {
@@ -102,7 +133,7 @@ __device__ __forceinline__ uint32_t block_exclusive_sum(uint32_t v, uint32_t* ws
   const int wid = threadIdx.x / kWave;
   const uint32_t incl = wave_inclusive_sum(v);
   if (lane == kWave - 1) wsum[wid] = incl;
-  __syncthreads();
+  block_sync_lds();
   uint32_t base = 0, tot = 0;
 #pragma unroll
   for (int w = 0; w < NT / kWave; ++w) {
@@ -110,7 +141,7 @@ __device__ __forceinline__ uint32_t block_exclusive_sum(uint32_t v, uint32_t* ws
     base += (w < wid) ? s : 0u;
     tot += s;
   }
-  __syncthreads();
+  block_sync_lds();
   total = tot;
   return base + incl - v;
 }

@@ -40,7 +40,7 @@ __device__ __forceinline__ float wave_select_kth(const float* row, int n, int k,
     const uint32_t h[4] = {h4.x, h4.y, h4.z, h4.w};
     const uint32_t local = h[0] + h[1] + h[2] + h[3];
     const uint32_t incl = wave_inclusive_sum(local);
-    const uint32_t total = __shfl(incl, kWave - 1, kWave);
+    const uint32_t total = wave_read_lane(incl, kWave - 1);
     const uint32_t above = total - incl;  // keys in higher lanes' bins
     const bool mine = above < krem && above + local >= krem;
     uint32_t bucket = 0, knew = 0, cnt = 0;
