@@ -224,6 +224,36 @@ def cpu_baseline(budget_s=12.0):
     return res
 
 
+def pmc_workload(args, dev):
+    """Kernels whose FETCH_SIZE / WRITE_SIZE give the traffic figures: a plain
+    copy of known size (256 MiB read + 256 MiB written) first, so each
+    counter's reading per byte can be calibrated in the same run."""
+    import torch
+
+    import dsa_attention as D
+    from lightning_indexer import indexer_scores_hip
+    from topk_threshold import topk_threshold
+
+    x = torch.ones(64 * 1024 * 1024, device=dev)
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    y.copy_(x)
+    torch.cuda.synchronize()
+    del x, y
+    ins = gpu_inputs(C1, torch.float32, dev)
+    for _ in range(args.steps):
+        D.dsa_fused_hip(*ins, C1["k"])
+    torch.cuda.synchronize()
+    del ins
+    q, kk, w = gpu_inputs(C4, torch.bfloat16, dev, seed=4)[:3]
+    scores = indexer_scores_hip(q, kk, w, write_upper=False)
+    del q, kk, w
+    for _ in range(3):
+        topk_threshold(scores, C4["k"], causal=True)
+    torch.cuda.synchronize()
+    log("pmc workload done")
+
+
 def traffic_from_profile():
     path = os.path.join(ROOT, "profiles", "fused_c1_traffic.json")
     if os.path.exists(path):
@@ -240,6 +270,10 @@ def main():
     ap.add_argument("--mode", choices=("graph", "eager"), default="graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-select", action="store_true", help="skip the config-4 select leg")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="run only the workload profiled for HBM traffic: one 256 MiB "
+                         "device-to-device copy (counter calibration), then --steps eager "
+                         "fused launches at config 1 and 3 causal selects at config 4")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build has no "
@@ -249,6 +283,9 @@ def main():
     import torch
 
     dev = torch.device("cuda:0")
+    if args.pmc_workload:
+        pmc_workload(args, dev)
+        return
     B, T = C1["B"], C1["T"]
     log("bench: fused config 1")
     elapsed, kern_s = bench_fused(args, dev)

@@ -3,7 +3,7 @@
 //   sel(s)   = s <= t  &&  score[s] >= thr                (dsa_attention.py:45-46, :258)
 //   O[h,:]   = sum_{s in sel} softmax_s(<Q[t,h],K[s,h]> * scale) * V[s,h,:]
 //
-// The wave scans the score row 256 entries at a time (a float4 per lane),
+// The wave scans the score row 512 entries at a time (two float4 per lane),
 // compacts the selected key positions in index order into a per-wave LDS
 // list (ballot-free: a wave prefix sum of per-lane counts), then gathers
 // only those K/V rows.  Each K (or V) row is HQ*D contiguous elements; lane
@@ -19,7 +19,7 @@
 
 namespace dsa {
 
-constexpr int kListCap = 256;  // one 256-entry segment of the score row
+constexpr int kListCap = 512;  // one 512-entry segment of the score row
 
 // Q/K/V point at this batch element: Q row t is Q + t*HQ*DQ, etc.
 // load4(s, sv) loads scores s..s+3 (s <= t, s % 4 == 0) of this query's row.
@@ -56,25 +56,25 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
   float m = -__builtin_huge_valf();
   float lsum = 0.f;
 
-  // Logit (log2 domain) of key s for this lane's V head.
+  // Keys gathered per round trip: as many as fit ~64 registers of K+V.
+  constexpr int U = (EK + EV <= 4) ? 16 : (EK + EV <= 8) ? 8 : (EK + EV <= 16) ? 4 : 2;
+  // Processes keys ss[0..nu) (nu <= U): all their K/V rows are loaded before
+  // any is used, so a group costs one memory round trip.
   auto process = [&](const int* ss, int nu) {
-    constexpr int U = (EK <= 8) ? 4 : 2;
     float kv[U][EK];
     float vv[U][EV];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (u < nu) {
-        const int64_t s = ss[u];
-        if (kact) load_cvt<Tag, EK>(K + s * EQ + lane * EK, kv[u]);
-        else {
+      const int64_t s = ss[u < nu ? u : 0];
+      if (kact && u < nu) load_cvt<Tag, EK>(K + s * EQ + lane * EK, kv[u]);
+      else {
 #pragma unroll
-          for (int e = 0; e < EK; ++e) kv[u][e] = 0.f;
-        }
-        if (vact) load_cvt<Tag, EV>(V + s * EVt + lane * EV, vv[u]);
-        else {
+        for (int e = 0; e < EK; ++e) kv[u][e] = 0.f;
+      }
+      if (vact && u < nu) load_cvt<Tag, EV>(V + s * EVt + lane * EV, vv[u]);
+      else {
 #pragma unroll
-          for (int e = 0; e < EV; ++e) vv[u][e] = 0.f;
-        }
+        for (int e = 0; e < EV; ++e) vv[u][e] = 0.f;
       }
     }
     float lg[U];
@@ -113,14 +113,25 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
     m = mnew;
   };
 
-  for (int s0 = 0; s0 <= t; s0 += 4 * kWave) {
-    const int sb = s0 + 4 * lane;
-    float sv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (sb <= t) load4(sb, sv);
-    int cnt = 0;
-    bool keep[4];
+  for (int s0 = 0; s0 <= t; s0 += kListCap) {
+    // Lane l scans entries s0 + 8l .. s0 + 8l + 7 (two float4).
+    const int sb = s0 + 8 * lane;
+    float sv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (sb <= t) {
+      float a4[4];
+      load4(sb, a4);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < 4; ++c) sv[c] = a4[c];
+      if (sb + 4 <= t) {
+        load4(sb + 4, a4);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) sv[4 + c] = a4[c];
+      }
+    }
+    int cnt = 0;
+    bool keep[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
       keep[c] = (sb + c <= t) && (sv[c] >= thr);
       cnt += keep[c] ? 1 : 0;
     }
@@ -128,13 +139,10 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
     const int total = wave_read_lane(incl, kWave - 1);
     int p = incl - cnt;
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < 8; ++c)
       if (keep[c]) list[p++] = sb + c;
     wave_lds_sync();
-    constexpr int U = (EK <= 8) ? 4 : 2;
-    int i = 0;
-    for (; i + U <= total; i += U) process(list + i, U);
-    for (; i < total; ++i) process(list + i, 1);
+    for (int i = 0; i < total; i += U) process(list + i, min(U, total - i));
     wave_lds_sync();
   }
 

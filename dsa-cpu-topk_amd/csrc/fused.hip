@@ -12,7 +12,7 @@
 //
 // LDS per block: 16 score rows of RS floats, RS = round_up(T,32) + 16 (the
 // +16 puts consecutive rows on different banks for the MFMA epilogue
-// stores), plus a 256-bin histogram and a 256-entry key list per wave.
+// stores), plus a 256-bin histogram and a 512-entry key list per wave.
 #include "attn_tile.h"
 #include "dsa_launch.h"
 #include "indexer_tile.h"

@@ -121,8 +121,9 @@ __device__ __forceinline__ void indexer_rows(const typename Tag::raw* __restrict
   };
   if (nhg == 1) load_a(0, a_cached, w_cached);
 
-  for (int s0 = s_begin; s0 < s_end; s0 += 16 * KB) {
-    S bk[KB];
+  // Key blocks of super-block s0 -> registers.  The next super-block is
+  // loaded while the MFMAs of the current one run.
+  auto load_b = [&](int s0, S (&bk)[KB]) {
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
       const int s = s0 + 16 * kb + r16;
@@ -131,6 +132,12 @@ __device__ __forceinline__ void indexer_rows(const typename Tag::raw* __restrict
       else
         bk[kb].zero();
     }
+  };
+  S bk[KB];
+  load_b(s_begin, bk);
+  for (int s0 = s_begin; s0 < s_end; s0 += 16 * KB) {
+    S bn[KB];
+    if (s0 + 16 * KB < s_end) load_b(s0 + 16 * KB, bn);
     float sc[KB];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) sc[kb] = 0.f;
@@ -160,6 +167,8 @@ __device__ __forceinline__ void indexer_rows(const typename Tag::raw* __restrict
       }
     }
     sink(s0, sc);
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) bk[kb] = bn[kb];
   }
 }
 
