@@ -200,13 +200,18 @@ __device__ __forceinline__ void load_cvt(const typename Tag::raw* __restrict__ p
   }
 }
 
-// XCD-aware block order.  Workgroups are dispatched round-robin over the 8
-// XCDs (block i runs on XCD i % 8).  Remap so that XCD x works through a
-// contiguous range of logical blocks -- neighbouring logical blocks share K/V
-// rows and hit the same L2.  Identity when nblocks is not a multiple of 8.
-__device__ __forceinline__ uint32_t xcd_swizzle(uint32_t bid, uint32_t nblocks) {
-  if ((nblocks & 7u) != 0u) return bid;
-  return (bid & 7u) * (nblocks >> 3) + (bid >> 3);
+// Block order for causal work whose cost grows with the query tile.
+// Workgroups are dispatched in index order, round-robin over the 8 XCDs
+// (block i starts on XCD i % 8).  Index order here is: tiles longest first,
+// batch element fastest.  So every XCD receives the same mix of long and
+// short tiles (a contiguous tile range per XCD would leave the XCD holding
+// the last rows of a causal triangle with up to 2x the average work), and
+// when B is a multiple of 8 each XCD receives B/8 whole batch elements, whose
+// K/V rows then stay in that XCD's L2.
+__device__ __forceinline__ void causal_block_tile(uint32_t bid, int64_t B, int ntile,
+                                                  int64_t& b, int& tile) {
+  b = static_cast<int64_t>(bid) % B;
+  tile = ntile - 1 - static_cast<int>(static_cast<int64_t>(bid) / B);
 }
 
 }  // namespace dsa

@@ -7,8 +7,8 @@
 //   3. per row, sparse attention over keys with score >= thr (attn_tile.h)
 // The score rows never touch HBM.  The 4 waves of a block hold 16
 // consecutive queries and share nothing but L1, so there is no block barrier;
-// blocks run longest queries first and batch elements map to XCDs in
-// contiguous ranges (K/V of a batch element stays in one L2).
+// blocks run longest queries first, spread evenly over the XCDs
+// (causal_block_tile).
 //
 // LDS per block: 16 score rows of RS floats, RS = round_up(T,32) + 16 (the
 // +16 puts consecutive rows on different banks for the MFMA epilogue
@@ -52,9 +52,9 @@ __global__ __launch_bounds__(256) void fused_kernel(FusedArgs a) {
   const int T = a.T;
   const int RS = a.RS;
   const int tiles = (T + 15) >> 4;
-  const uint32_t L = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int64_t b = L / tiles;
-  const int tile = tiles - 1 - static_cast<int>(L % tiles);
+  int64_t b;
+  int tile;
+  causal_block_tile(blockIdx.x, a.B, tiles, b, tile);
   const int t0 = tile * 16 + wave * 4;
   if (t0 >= T) return;
 

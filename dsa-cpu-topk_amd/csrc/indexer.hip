@@ -5,11 +5,26 @@
 // above the diagonal (written only on request -- the public drop-in asks for
 // it because callers check it, the internal split pipeline does not).
 //
-// Grid: x = (batch, 16-query tile), y = 256-key chunk.  Each of the 4 waves
-// owns 4 queries of the tile and walks the chunk in super-blocks of 16*KB
-// keys (indexer_tile.h).  Chunks wholly above the diagonal do no MFMA work;
-// they only write -inf when asked, which is what the reference's kernel
-// computes for those tiles anyway (lightning_indexer.py:92-94).
+// Two kernels:
+//
+// indexer_qtile_kernel (query-stationary; used whenever a 4-query tile of q
+//   fits in LDS).  A block owns TQ = 4*NQ consecutive queries of one batch
+//   element.  It stages their q rows (all heads) into LDS once, already in
+//   MFMA fragment order, so every later A-operand read is one conflict-free
+//   ds_read_b128 per lane, and their w rows next to them.  Its 8 waves then
+//   split the causal key range [0, t0+TQ) into super-blocks of 16*KB keys,
+//   load each super-block's k rows straight into B-operand registers
+//   (prefetching the next), and run all TQ queries x HI heads against it.  q
+//   is read from HBM exactly once; k (B*T*DI elements) is re-read from L2 /
+//   MALL once per query tile.
+//
+// indexer_kernel (register-streaming; fallback for very wide q rows).  Grid
+//   x = (batch, 16-query tile), y = 256-key chunk; each wave owns 4 queries
+//   and walks its chunk with indexer_rows (indexer_tile.h).
+//
+// Both skip key blocks wholly above the diagonal (no MFMA work there); they
+// only write -inf when asked, which is what the reference's kernel computes
+// for those tiles anyway (lightning_indexer.py:92-94).
 #include "dsa_launch.h"
 #include "indexer_tile.h"
 
@@ -73,8 +88,265 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Query-stationary kernel.
+// ---------------------------------------------------------------------------
+constexpr int kQWaves = 8;
+#ifndef DSA_QTILE_MAX_NQ
+#define DSA_QTILE_MAX_NQ 4
+#endif
+constexpr size_t kQTileLds = 160 * 1024;  // q + w tile budget per block (all of a CU's LDS)
+
+// 16-byte chunks of one lane's DI/4-element operand slice.
+template <typename Tag, int DI>
+constexpr int lane_chunks() { return (DI / 4) * Tag::kBytes / 16; }
+
+// max(x, 0) on the bit pattern: a float with the sign bit set is a negative
+// int32.  One integer max instead of the canonicalising float max the
+// compiler emits for fmaxf on values it cannot prove canonical (MFMA
+// results); -0.0 maps to +0.0, a NaN with the sign bit clear stays NaN.
+__device__ __forceinline__ float relu(float x) {
+  return __int_as_float(max(__float_as_int(x), 0));
+}
+
+// One 16-byte A chunk against the matching chunk of a key block's B slice.
+template <typename Tag, int E>
+__device__ __forceinline__ f32x4 mfma_chunk(const uint4& a, const Slice<Tag, E>& b, int c,
+                                            f32x4 acc) {
+  if constexpr (Tag::kBytes == 4) {
+    const float av[4] = {__uint_as_float(a.x), __uint_as_float(a.y), __uint_as_float(a.z),
+                         __uint_as_float(a.w)};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], b.v[4 * c + j], acc, 0, 0, 0);
+    return acc;
+  } else if constexpr (__is_same(Tag, BF16)) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b.v[c]), acc, 0,
+                                                   0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b.v[c]), acc, 0, 0,
+                                                  0);
+  }
+}
+
+struct QTileShape {
+  int nq;   // quads (4 queries) per block
+  int nhg;  // head groups of 4 (HI rounded up)
+};
+
+template <typename Tag, int DI>
+size_t qtile_lds_bytes(QTileShape sh) {
+  return static_cast<size_t>(sh.nq) * sh.nhg * (lane_chunks<Tag, DI>() * 1024 + 64);
+}
+
+// LDS layout:
+//   qf[quad][hg][chunk][lane] : uint4   A fragment of lane `lane`: row r16 =
+//       (query 4*quad + r16/4, head 4*hg + r16%4), chunk `chunk` of the
+//       lane group's DI slice (lane/16 owns dims [lane/16*DI/4, ...))
+//   wf[quad][hg][g][4]        : float   w of query 4*quad+g, heads 4hg..4hg+3
+template <typename Tag, int DI, int KB, int NQ>
+__global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs a) {
+  using raw = typename Tag::raw;
+  using S = Slice<Tag, DI / 4>;
+  constexpr int NCH = lane_chunks<Tag, DI>();
+  constexpr int E = DI / 4;
+  constexpr int EPC = 16 / Tag::kBytes;  // elements per 16-byte chunk
+  extern __shared__ __align__(16) uint4 lds[];
+  const int T = a.T;
+  const int HI = a.HI;
+  const int nhg = (HI + 3) >> 2;
+  constexpr int TQ = 4 * NQ;
+  const int ntile = (T + TQ - 1) / TQ;
+  int64_t b;
+  int tile;
+  causal_block_tile(blockIdx.x, a.B, ntile, b, tile);  // longest rows first
+  const int t0 = tile * TQ;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = lane_id();
+  const int g = lane >> 4, r16 = lane & 15;
+
+  const raw* q = static_cast<const raw*>(a.q) + b * T * static_cast<int64_t>(HI) * DI;
+  const raw* k = static_cast<const raw*>(a.k) + b * T * static_cast<int64_t>(DI);
+  const raw* w = static_cast<const raw*>(a.w) + b * T * static_cast<int64_t>(HI);
+  float* out = a.scores + (b * T) * a.ld;
+
+  uint4* qf = lds;
+  float* wf = reinterpret_cast<float*>(lds + static_cast<size_t>(NQ) * nhg * NCH * 64);
+
+  // Stage q: one 16-byte chunk per thread-iteration, coalesced along DI.
+  {
+    const int hp4 = 4 * nhg;
+    const int per_t = hp4 * (DI / EPC);
+    const int total = TQ * per_t;
+    for (int u = tid; u < total; u += 64 * kQWaves) {
+      const int tl = u / per_t;
+      const int rem = u - tl * per_t;
+      const int h = rem / (DI / EPC);
+      const int d0 = (rem - h * (DI / EPC)) * EPC;
+      const int t = t0 + tl;
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (t < T && h < HI)
+        v = *reinterpret_cast<const uint4*>(q + (static_cast<int64_t>(t) * HI + h) * DI + d0);
+      const int gg = d0 / E;
+      const int c = (d0 - gg * E) / EPC;
+      const int ln = gg * 16 + 4 * (tl & 3) + (h & 3);
+      qf[((static_cast<size_t>(tl >> 2) * nhg + (h >> 2)) * NCH + c) * 64 + ln] = v;
+    }
+    for (int u = tid; u < TQ * hp4; u += 64 * kQWaves) {
+      const int tl = u / hp4;
+      const int h = u - tl * hp4;
+      const int t = t0 + tl;
+      const float wv = (t < T && h < HI) ? to_f32(Tag{}, w[static_cast<int64_t>(t) * HI + h]) : 0.f;
+      wf[((tl >> 2) * nhg + (h >> 2)) * 16 + (tl & 3) * 4 + (h & 3)] = wv;
+    }
+  }
+  __syncthreads();
+
+  const float ninf = -__builtin_huge_valf();
+  const int t_end = (t0 + TQ < T) ? t0 + TQ : T;  // keys [0, t_end) can be causal
+  constexpr int SB = 16 * KB;
+  const int nsb = (t_end + SB - 1) / SB;
+
+  // k rows of super-block sb into B registers.  Rows past T (and whole
+  // super-blocks past the last one, loaded as prefetch) are clamped to row
+  // T-1: their scores are never stored, and unconditional loads keep the
+  // wait counts exact so the prefetch stays in flight during the MFMAs.
+  auto load_b = [&](int sbi, S (&bk)[KB]) {
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      const int s = min(sbi * SB + 16 * kb + r16, T - 1);
+      bk[kb].load(k + static_cast<int64_t>(s) * DI + g * E);
+    }
+  };
+
+  // All NQ quads against one super-block.  The head-group loop holds no
+  // stores: a loop with stores and no loads makes the compiler drain every
+  // outstanding load (the prefetch included) before entering it.
+  auto compute = [&](int sbi, const S (&bk)[KB]) {
+    const int s0 = sbi * SB;
+    float sc[NQ][KB];
+#pragma unroll
+    for (int qd = 0; qd < NQ; ++qd)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) sc[qd][kb] = 0.f;
+    const uint4* qa = qf + lane;
+    const float4* wq = reinterpret_cast<const float4*>(wf) + g;
+    for (int hg = 0; hg < nhg; ++hg) {
+#pragma unroll
+      for (int qd = 0; qd < NQ; ++qd) {
+        f32x4 acc[KB];
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) acc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          const uint4 av = qa[((qd * nhg + hg) * NCH + c) * 64];
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) acc[kb] = mfma_chunk<Tag, E>(av, bk[kb], c, acc[kb]);
+        }
+        const float4 wv = wq[(qd * nhg + hg) * 4];
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          sc[qd][kb] = fmaf(wv.x, relu(acc[kb][0]), sc[qd][kb]);
+          sc[qd][kb] = fmaf(wv.y, relu(acc[kb][1]), sc[qd][kb]);
+          sc[qd][kb] = fmaf(wv.z, relu(acc[kb][2]), sc[qd][kb]);
+          sc[qd][kb] = fmaf(wv.w, relu(acc[kb][3]), sc[qd][kb]);
+        }
+      }
+    }
+#pragma unroll
+    for (int qd = 0; qd < NQ; ++qd) {
+      const int tq = t0 + 4 * qd + g;  // this lane's output query
+      if (tq < T) {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          const int s = s0 + 16 * kb + r16;
+          if (s < T && (s <= tq || a.write_upper))
+            out[static_cast<int64_t>(tq) * a.ld + s] = (s <= tq) ? sc[qd][kb] : ninf;
+        }
+      }
+    }
+  };
+
+  // Ping-pong over two register sets: compute on one while the other loads.
+  const int last = nsb - 1;
+  S b0[KB], b1[KB];
+  int sb = wave;
+  load_b(min(sb, last), b0);
+  while (sb < nsb) {
+    load_b(min(sb + kQWaves, last), b1);
+    compute(sb, b0);
+    sb += kQWaves;
+    if (sb >= nsb) break;
+    load_b(min(sb + kQWaves, last), b0);
+    compute(sb, b1);
+    sb += kQWaves;
+  }
+
+  // Keys past the last super-block are above the diagonal for every query.
+  if (a.write_upper) {
+    const int s_lo = nsb * SB;
+    const int width = T - s_lo;
+    if (width > 0) {
+      for (int tl = wave; tl < TQ; tl += kQWaves) {
+        const int t = t0 + tl;
+        if (t >= T) break;
+        for (int s = s_lo + lane; s < T; s += 64) out[static_cast<int64_t>(t) * a.ld + s] = ninf;
+      }
+    }
+  }
+}
+
+template <typename Tag, int DI, int KB, int NQ>
+hipError_t launch_qtile(const IndexerArgs& a, QTileShape sh, hipStream_t stream) {
+  auto kern = indexer_qtile_kernel<Tag, DI, KB, NQ>;
+  const size_t lds = qtile_lds_bytes<Tag, DI>(sh);
+  static const bool attr_set = [&] {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(kQTileLds));
+    if (e != hipSuccess) (void)hipGetLastError();
+    return e == hipSuccess;
+  }();
+  (void)attr_set;
+  const int64_t nblk = a.B * ((a.T + 4 * NQ - 1) / (4 * NQ));
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(nblk)), dim3(64 * kQWaves), lds, stream,
+                     a);
+  return hipGetLastError();
+}
+
+// Largest quad count (<= DSA_QTILE_MAX_NQ) whose q + w tile fits the LDS
+// budget; 0 when one quad does not fit.
+template <typename Tag, int DI>
+QTileShape pick_qtile(const IndexerArgs& a) {
+  QTileShape sh{0, (a.HI + 3) / 4};
+  for (int nq = DSA_QTILE_MAX_NQ; nq >= 1; nq >>= 1) {
+    if (qtile_lds_bytes<Tag, DI>(QTileShape{nq, sh.nhg}) <= kQTileLds) {
+      sh.nq = nq;
+      break;
+    }
+  }
+  return sh;
+}
+
+template <typename Tag, int DI, int KB>
+hipError_t launch_stream(const IndexerArgs& a, hipStream_t stream);
+
 template <typename Tag, int DI, int KB>
 hipError_t launch(const IndexerArgs& a, hipStream_t stream) {
+  const QTileShape sh = pick_qtile<Tag, DI>(a);
+  switch (sh.nq) {
+    case 4: return launch_qtile<Tag, DI, KB, 4>(a, sh, stream);
+    case 2: return launch_qtile<Tag, DI, KB, 2>(a, sh, stream);
+    case 1: return launch_qtile<Tag, DI, KB, 1>(a, sh, stream);
+  }
+  return launch_stream<Tag, DI, KB>(a, stream);
+}
+
+template <typename Tag, int DI, int KB>
+hipError_t launch_stream(const IndexerArgs& a, hipStream_t stream) {
   const int ntile = (a.T + 15) / 16;
   const dim3 grid(static_cast<unsigned>(a.B * ntile), static_cast<unsigned>((a.T + kChunk - 1) / kChunk));
   hipLaunchKernelGGL((indexer_kernel<Tag, DI, KB>), grid, dim3(256), 0, stream, a);

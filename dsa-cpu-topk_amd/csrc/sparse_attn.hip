@@ -6,10 +6,8 @@
 // reference loads every K/V row of the prefix and masks; this kernel reads
 // only the score row and the selected K/V rows (attn_tile.h).
 //
-// Block = 4 waves = 4 consecutive queries of one batch element.  Blocks are
-// ordered longest query first within each batch element, and the batch
-// elements are spread over the XCDs in contiguous ranges so the K/V rows a
-// batch element gathers stay in one XCD's L2.
+// Block = 4 waves = 4 consecutive queries of one batch element.  Blocks run
+// longest query first, spread evenly over the XCDs (causal_block_tile).
 #include "attn_tile.h"
 #include "dsa_launch.h"
 
@@ -38,9 +36,9 @@ __global__ __launch_bounds__(256) void sparse_attn_kernel(AttnArgs a) {
   const int wave = threadIdx.x >> 6;
   const int T = a.T;
   const int tiles = (T + 3) >> 2;
-  const uint32_t L = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int64_t b = L / tiles;
-  const int tile = tiles - 1 - static_cast<int>(L % tiles);
+  int64_t b;
+  int tile;
+  causal_block_tile(blockIdx.x, a.B, tiles, b, tile);
   const int t = tile * 4 + wave;
   if (t >= T) return;
   const int64_t EQ = static_cast<int64_t>(a.HQ) * a.DQ;

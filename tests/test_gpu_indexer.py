@@ -52,6 +52,15 @@ def test_shapes_16bit(dev, dtype, B, T, HI, DI):
     run_case(dev, B, T, HI, DI, dtype=dtype, rtol=2e-2, atol=2e-2)
 
 
+@pytest.mark.parametrize("dtype,B,T,HI,DI", [(torch.float32, 1, 80, 64, 256),
+                                              (torch.bfloat16, 2, 70, 160, 256)])
+def test_wide_q_rows_stream_kernel(dev, dtype, B, T, HI, DI):
+    """q rows too wide for a 4-query LDS tile (HI*DI*bytes > 40 KiB) take the
+    register-streaming kernel."""
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    run_case(dev, B, T, HI, DI, dtype=dtype, rtol=tol, atol=tol)
+
+
 def test_c3_shape_sampled_rows(dev):
     T = 4096
     rows = [0, 1, 15, 16, 255, 256, 1000, 2047, 4094, 4095]
