@@ -92,7 +92,8 @@ int dsa_topk_threshold(const float* scores, int64_t rows, int64_t n, int64_t ld,
  *   sel(b,t,s) = (s <= t) && (scores[b,t,s] >= thr[b*T+t])   (ties kept)
  *   O[b,t,h,:] = sum_{s in sel} softmax_s(<Q[b,t,h],K[b,s,h]> * scale) V[b,s,h,:]
  * Rows that select nothing (only possible for a NaN or +inf threshold) get
- * O = 0.  The threshold may come from anywhere (the reference's hybrid path
+ * O = NaN, the 0/0 of a softmax over an all -inf row, as in the reference's
+ * kernel and torch path.  The threshold may come from anywhere (the reference's hybrid path
  * computes it on the CPU, dsa_hybrid.py:61-66).
  * Replaces: _sparse_attn_kernel + sparse_attention_with_threshold_triton,
  *           reference dsa_attention.py:234-324.
