@@ -16,7 +16,7 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libdsa_amd.so")
-SOURCES = ["capi.cpp", "topk.hip", "indexer.hip", "sparse_attn.hip", "fused.hip"]
+SOURCES = ["capi.cpp", "topk.hip", "indexer.hip", "sparse_attn.hip", "tile_attn.hip", "fused.hip"]
 
 HIPFLAGS = [
     "--offload-arch=gfx950",

@@ -121,6 +121,28 @@ int dsa_sparse_attn_threshold(const float* scores, int64_t ld, const float* thr,
                     "dsa_sparse_attn_threshold");
 }
 
+int dsa_sparse_attn_threshold_tiled(const float* scores, int64_t ld, const float* thr,
+                                    const void* Q, const void* K, const void* V, int dtype,
+                                    int64_t B, int64_t T, int HQ, int DQ, int DV, float scale,
+                                    float* out, void* stream) {
+  if (!dtype_ok(dtype)) return fail(DSA_EINVAL, "sparse_attn_tiled: unknown dtype %d", dtype);
+  if (B < 0 || T < 0) return fail(DSA_EINVAL, "sparse_attn_tiled: negative size");
+  if (T > kMaxElems) return fail(DSA_EINVAL, "sparse_attn_tiled: T=%lld too large", (long long)T);
+  if (HQ < 1 || HQ > 1024) return fail(DSA_EINVAL, "sparse_attn_tiled: HQ=%d outside [1,1024]", HQ);
+  if (ld < T) return fail(DSA_EINVAL, "sparse_attn_tiled: ld=%lld < T=%lld", (long long)ld, (long long)T);
+  if (!std::isfinite(scale)) return fail(DSA_EINVAL, "sparse_attn_tiled: scale must be finite");
+  if (dtype == DSA_F32 || DQ != DV || (DQ != 64 && DQ != 128))
+    return fail(DSA_EUNSUPPORTED, "sparse_attn_tiled: needs bf16/fp16 and DQ = DV in {64,128} (dtype %d DQ=%d DV=%d)", dtype, DQ, DV);
+  if (B * T == 0) return DSA_OK;
+  if (!scores || !thr || !Q || !K || !V || !out) return fail(DSA_EINVAL, "sparse_attn_tiled: null pointer");
+  if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(out))
+    return fail(DSA_EINVAL, "sparse_attn_tiled: Q/K/V/out must be 16-byte aligned");
+  if (B * T * HQ * static_cast<int64_t>(DQ) > (int64_t{1} << 40)) return fail(DSA_EINVAL, "sparse_attn_tiled: Q too large");
+  return hip_status(dsa::launch_tile_attn(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, scale,
+                                          out, static_cast<hipStream_t>(stream)),
+                    "dsa_sparse_attn_threshold_tiled");
+}
+
 int dsa_fused_forward(const void* q_idx, const void* k_idx, const void* w_idx, const void* Q,
                       const void* K, const void* V, int dtype, int64_t B, int64_t T, int HI,
                       int DI, int HQ, int DQ, int DV, int top_k, float scale, float* out,

@@ -25,6 +25,15 @@ hipError_t launch_sparse_attn(const float* scores, int64_t ld, const float* thr,
                               hipStream_t stream);
 bool sparse_attn_supported(int dtype, int HQ, int DQ, int DV);
 
+// The same attention as dense-masked MFMA tiles (tile_attn.hip).  The
+// threshold entry point switches to it at T >= kTiledMinT when it applies.
+constexpr int64_t kTiledMinT = 4096;
+bool tile_attn_supported(int dtype, int HQ, int DQ, int DV, const void* Q, const void* K,
+                         const void* V);
+hipError_t launch_tile_attn(const float* scores, int64_t ld, const float* thr, const void* Q,
+                            const void* K, const void* V, int dtype, int64_t B, int64_t T, int HQ,
+                            int D, float scale, float* out, hipStream_t stream);
+
 // Fused forward for T <= kFusedMaxT.
 constexpr int64_t kFusedMaxT = 2048;
 hipError_t launch_fused(const void* qi, const void* ki, const void* wi, const void* Q,

@@ -8,6 +8,11 @@
 //
 // Block = 4 waves = 4 consecutive queries of one batch element.  Blocks run
 // longest query first, spread evenly over the XCDs (causal_block_tile).
+//
+// For long rows (T >= kTiledMinT) with 16-bit inputs and DQ = DV in {64,
+// 128}, launch_sparse_attn hands over to the dense-masked MFMA tile kernel
+// (tile_attn.hip): there every query selects a large share of a long row and
+// per-query gathers would re-read the same K/V rows thousands of times.
 #include "attn_tile.h"
 #include "dsa_launch.h"
 
@@ -110,6 +115,8 @@ hipError_t launch_sparse_attn(const float* scores, int64_t ld, const float* thr,
                               int HQ, int DQ, int DV, float scale, float* out,
                               hipStream_t stream) {
   if (B == 0 || T == 0) return hipSuccess;
+  if (T >= kTiledMinT && tile_attn_supported(dtype, HQ, DQ, DV, Q, K, V))
+    return launch_tile_attn(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, scale, out, stream);
   const bool vec = (ld % 4 == 0) && ((reinterpret_cast<uintptr_t>(scores) & 15u) == 0);
   AttnArgs a{scores, ld, thr, Q, K, V, B, static_cast<int>(T), HQ, DQ, DV,
              scale * 1.4426950408889634f, out, vec ? 1 : 0};

@@ -75,9 +75,14 @@ def _attn_inputs(Q, K, V):
 
 
 def sparse_attention_hip(scores: torch.Tensor, threshold: torch.Tensor, Q, K, V,
-                         out: torch.Tensor | None = None) -> torch.Tensor:
+                         out: torch.Tensor | None = None, tiled: bool = False) -> torch.Tensor:
     """Sparse attention for any T given scores [B,T,T] fp32 and threshold
-    [B,T,1] (or [B,T]); only entries s <= t of each score row are read."""
+    [B,T,1] (or [B,T]); only entries s <= t of each score row are read.
+
+    The library picks the kernel: per-query gathers, or -- for T >= 4096
+    with 16-bit Q/K/V and DQ = DV in {64, 128} -- dense-masked MFMA tiles.
+    tiled=True runs the tile kernel at any T (AssertionError for shapes it
+    does not cover)."""
     L.require_gpu(scores, threshold, Q, K, V)
     B, T, _ = scores.shape
     HQ, DQ = Q.shape[-2], Q.shape[-1]
@@ -90,7 +95,8 @@ def sparse_attention_hip(scores: torch.Tensor, threshold: torch.Tensor, Q, K, V,
     dt, Q, K, V = _attn_inputs(Q, K, V)
     if out is None:
         out = torch.empty(B, T, HQ, DV, device=Q.device, dtype=torch.float32)
-    rc = L.lib().dsa_sparse_attn_threshold(
+    fn = L.lib().dsa_sparse_attn_threshold_tiled if tiled else L.lib().dsa_sparse_attn_threshold
+    rc = fn(
         scores.data_ptr(), T, thr.data_ptr(), Q.data_ptr(), K.data_ptr(), V.data_ptr(),
         L.dtype_code(dt), B, T, HQ, DQ, DV, 1.0 / math.sqrt(DQ), out.data_ptr(),
         L.stream_ptr(Q.device))

@@ -106,6 +106,25 @@ int dsa_sparse_attn_threshold(const float* scores, int64_t ld, const float* thr,
                               int DV, float scale, float* out, void* stream);
 
 /*
+ * dsa_sparse_attn_threshold computed as dense-masked MFMA tiles: the same
+ * sel and O, evaluated over the causal triangle in 128-query x 64-key tiles
+ * with the selection as a mask, so every K/V tile a block loads serves 128
+ * queries.  dsa_sparse_attn_threshold switches to it by itself for
+ * T >= 4096 when the shape qualifies; this entry point runs it at any T.
+ * P is rounded to the 16-bit input type for the P.V product (fp32
+ * accumulation), inside the 16-bit tolerance.
+ * Replaces: _sparse_attn_kernel + sparse_attention_with_threshold_triton,
+ *           reference dsa_attention.py:234-324 (same contract as above).
+ * Constraints: bf16/fp16 Q/K/V; DQ = DV in {64,128}; 1 <= HQ <= 1024;
+ *   ld >= T; Q, K, V, out 16-byte aligned.  Other shapes return
+ *   DSA_EUNSUPPORTED.
+ */
+int dsa_sparse_attn_threshold_tiled(const float* scores, int64_t ld, const float* thr,
+                                    const void* Q, const void* K, const void* V,
+                                    int dtype, int64_t B, int64_t T, int HQ, int DQ,
+                                    int DV, float scale, float* out, void* stream);
+
+/*
  * Fused DSA forward for T <= 2048: indexer -> per-row radix select ->
  * sparse attention in one kernel; the score rows live in LDS only.
  * Same result as dsa_indexer_scores + dsa_topk_threshold(k = min(top_k,T),

@@ -15,14 +15,15 @@ pytestmark = pytest.mark.gpu
 
 
 def run_case(dev, B, T, HQ, DQ, DV, thr_fn, dtype=torch.float32, rtol=1e-4, atol=1e-4,
-             seed0=0, rows=None):
-    say(f"attn B={B} T={T} HQ={HQ} DQ={DQ} DV={DV} {dtype}")
+             seed0=0, rows=None, tiled=False):
+    say(f"attn B={B} T={T} HQ={HQ} DQ={DQ} DV={DV} {dtype} tiled={tiled}")
     _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, HQ, DQ, DV, dtype=dtype, seed0=seed0)
     g = torch.Generator().manual_seed(seed0 + 17)
     scores = torch.randn(B, T, T, generator=g)
     scores = torch.where(torch.rand(B, T, T, generator=g) < 0.1, 0.0, scores)   # ties at 0
     thr = thr_fn(scores)
-    out = sparse_attention_hip(scores.to(dev), thr.to(dev), Q.to(dev), K.to(dev), V.to(dev))
+    out = sparse_attention_hip(scores.to(dev), thr.to(dev), Q.to(dev), K.to(dev), V.to(dev),
+                               tiled=tiled)
     torch.cuda.synchronize()
     if rows is None:
         want = O.sparse_attn_threshold(scores, thr, Q, K, V)
@@ -104,3 +105,66 @@ def test_reference_wrapper_asserts_and_strided_threshold(dev):
                                                  K.to(dev), V.to(dev)).cpu()
     want = O.sparse_attn_threshold(s, topv[..., -1:], Q, K, V)
     assert close(out, want, 1e-4, 1e-4)[0]
+
+
+# --- dense-masked MFMA tile kernel (long rows; forced here at small T) ------
+BF, HF = torch.bfloat16, torch.float16
+
+
+@pytest.mark.parametrize("B,T,HQ,D,k,dtype", [(1, 128, 4, 64, 8, BF), (2, 300, 2, 128, 40, BF),
+                                              (1, 257, 1, 64, 16, HF), (2, 200, 16, 128, 20, BF),
+                                              (1, 1000, 3, 64, 100, HF), (1, 129, 2, 128, 200, BF)])
+def test_tiled_kth_threshold(dev, B, T, HQ, D, k, dtype):
+    """Ragged T (not a multiple of the 128-query / 64-key tiles), HQ not a
+    power of two, k > T (every causal key), both 16-bit types."""
+    run_case(dev, B, T, HQ, D, D, kth(k), dtype=dtype, rtol=2e-2, atol=2e-2, tiled=True)
+
+
+def test_tiled_external_thresholds(dev):
+    """-inf selects every causal key (dense causal attention); a diagonal
+    threshold keeps the keys scoring at least the s = t score."""
+    run_case(dev, 2, 260, 4, 64, 64, lambda s: torch.full(s.shape[:2] + (1,), -math.inf),
+             dtype=BF, rtol=2e-2, atol=2e-2, tiled=True)
+    run_case(dev, 2, 260, 4, 64, 64, lambda s: s.diagonal(0, 1, 2)[..., None].contiguous(),
+             dtype=BF, rtol=2e-2, atol=2e-2, tiled=True)
+
+
+def test_tiled_empty_selection_rows_are_nan(dev):
+    """Rows whose threshold nothing reaches (+inf, NaN) give 0/0 = NaN, as the
+    reference's softmax over an all -inf row; the other rows are unaffected."""
+    B, T, HQ, D = 1, 200, 2, 64
+    _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, HQ, D, D, dtype=BF)
+    s = torch.randn(B, T, T, generator=torch.Generator().manual_seed(5))
+    thr = kth(16)(s)
+    bad = torch.tensor([0, 7, 130, 199])
+    thr[0, bad[:2], 0] = math.inf
+    thr[0, bad[2:], 0] = math.nan
+    out = sparse_attention_hip(s.to(dev), thr.to(dev), Q.to(dev), K.to(dev), V.to(dev),
+                               tiled=True).cpu()
+    assert bool(torch.isnan(out[0, bad]).all())
+    good = torch.ones(T, dtype=torch.bool)
+    good[bad] = False
+    want = O.sparse_attn_threshold(s, thr, Q, K, V)
+    assert close(out[0, good], want[0, good], 2e-2, 2e-2)[0]
+
+
+def test_tiled_and_gather_agree(dev):
+    """Both kernels on the same bf16 inputs (config-4-like head shape)."""
+    B, T, HQ, D = 1, 700, 16, 128
+    _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, HQ, D, D, dtype=BF)
+    s = torch.randn(B, T, T, generator=torch.Generator().manual_seed(9))
+    thr = kth(64)(s)
+    args = (s.to(dev), thr.to(dev), Q.to(dev), K.to(dev), V.to(dev))
+    a = sparse_attention_hip(*args, tiled=True).cpu()
+    b = sparse_attention_hip(*args).cpu()
+    assert close(a, b, 2e-2, 2e-2)[0]
+
+
+def test_tiled_unsupported_shapes_raise(dev):
+    from _dsa_lib import DSAUnsupported
+
+    _, _, _, Q, K, V = O.make_inputs(1, 64, 1, 1, 4, 32, 32)
+    s = torch.randn(1, 64, 64)
+    with pytest.raises(DSAUnsupported):     # fp32 and D = 32 have no tile kernel
+        sparse_attention_hip(s.to(dev), kth(8)(s).to(dev), Q.to(dev), K.to(dev), V.to(dev),
+                             tiled=True)
