@@ -104,7 +104,8 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (u < nu) {
-        const float p = exp2f(lg[u] - mnew);
+        // bare v_exp_f32: results below 2^-126 flush to 0, which no sum can see
+        const float p = __builtin_amdgcn_exp2f(lg[u] - mnew);
         lsum += p;
 #pragma unroll
         for (int e = 0; e < EV; ++e) acc[e] = fmaf(p, vv[u][e], acc[e]);

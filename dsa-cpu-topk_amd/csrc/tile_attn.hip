@@ -65,10 +65,10 @@ struct Mfma16x16x32<BF16> {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
-    const __bf16 l = static_cast<__bf16>(lo), h = static_cast<__bf16>(hi);
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l)) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h)) << 16);
+  static __device__ __forceinline__ uint32_t pack(float lo, float hi) {  // one v_cvt_pk_bf16_f32
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), bf16x2));
   }
 };
 
@@ -79,9 +79,9 @@ struct Mfma16x16x32<F16> {
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
-    const _Float16 l = static_cast<_Float16>(lo), h = static_cast<_Float16>(hi);
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l)) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h)) << 16);
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), f16x2));
   }
 };
 
@@ -136,7 +136,9 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
       qf[qt][ks] = *reinterpret_cast<const uint4*>(Qb + tl * rowE + 32 * ks + 8 * g);
     thr[qt] = a.thr[b * T + tl];
   }
-  const float* srow0 = a.scores + (b * T) * a.ld;
+  const float* srow[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) srow[qt] = a.scores + (b * T + min(tq[qt], T - 1)) * a.ld;
 
   float m[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()};
   float l[2] = {0.f, 0.f};
@@ -152,22 +154,22 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
 
   // Global -> registers (prefetch) -> LDS staging of key tile kt.  Rows past
   // T are clamped to T-1: they are never causal for any query.
-  uint4 kreg[KCH];
-  uint4 vreg[VCH][2];
+  u32x4 kreg[KCH];  // native vectors: a uint4 struct array here stays in scratch memory
+  u32x4 vreg[VCH][2];
   auto gload = [&](int kt) {
     const int s0 = kt * kKT;
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
       const int c = tid + kNT * i;
       const int s = min(s0 + c / PPR, T - 1);
-      kreg[i] = *reinterpret_cast<const uint4*>(Kb + s * rowE + 8 * (c % PPR));
+      kreg[i] = *reinterpret_cast<const u32x4*>(Kb + s * rowE + 8 * (c % PPR));
     }
 #pragma unroll
     for (int i = 0; i < VCH; ++i) {
       const int c = tid + kNT * i;
       const int s = s0 + 2 * (c / PPR);
-      vreg[i][0] = *reinterpret_cast<const uint4*>(Vb + min(s, T - 1) * rowE + 8 * (c % PPR));
-      vreg[i][1] = *reinterpret_cast<const uint4*>(Vb + min(s + 1, T - 1) * rowE + 8 * (c % PPR));
+      vreg[i][0] = *reinterpret_cast<const u32x4*>(Vb + min(s, T - 1) * rowE + 8 * (c % PPR));
+      vreg[i][1] = *reinterpret_cast<const u32x4*>(Vb + min(s + 1, T - 1) * rowE + 8 * (c % PPR));
     }
   };
   auto swrite = [&](int buf) {
@@ -176,14 +178,13 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
       const int c = tid + kNT * i;
-      *reinterpret_cast<uint4*>(kl + (c / PPR) * KS + 8 * (c % PPR)) = kreg[i];
+      *reinterpret_cast<u32x4*>(kl + (c / PPR) * KS + 8 * (c % PPR)) = kreg[i];
     }
 #pragma unroll
     for (int i = 0; i < VCH; ++i) {
       const int c = tid + kNT * i;
       const int kp = c / PPR, d0 = 8 * (c % PPR);
-      const uint32_t w0[4] = {vreg[i][0].x, vreg[i][0].y, vreg[i][0].z, vreg[i][0].w};
-      const uint32_t w1[4] = {vreg[i][1].x, vreg[i][1].y, vreg[i][1].z, vreg[i][1].w};
+      const u32x4 w0 = vreg[i][0], w1 = vreg[i][1];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const uint32_t lo = (w0[e >> 1] >> (16 * (e & 1))) & 0xffffu;
@@ -198,40 +199,48 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
     const int buf = kt & 1;
     swrite(buf);
     block_sync_lds();
-    if (kt + 1 < nkt) gload(kt + 1);
+    gload(min(kt + 1, nkt - 1));  // unconditional: keeps the prefetch registers out of memory
     const int s0 = kt * kKT;
     if (s0 > wave_last) continue;  // the whole tile is above this wave's diagonal
 
-    // Selection mask, one bit per (qt, j, r): lane holds query tq[qt], keys
-    // s0 + 16j + 4g + r.
-    uint32_t selbits = 0u;
+    // Selection of this wave's 32 x 64 tile, as a per-entry bias word:
+    // 0.0f where (query tq[qt], key s0 + 16j + 4g + r) is selected, all-ones
+    // (a NaN) where not.  st + bias is st or NaN, which fmaxf skips, and
+    // v_bfi(bias, -inf, st) is st or -inf: both exact for any st, NaN and
+    // +-inf logits of unselected keys included (the reference masks them to
+    // -inf before its softmax).
+    const bool inner = (s0 + kKT - 1 <= tw) && (tw + 31 < T);  // no causal or row-end test
+    uint32_t bias[2][4][4];
+    bool any = false;
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int s = s0 + 16 * j + 4 * g;
-        const bool live = tq[qt] < T && s <= tq[qt];
-        float4 sv = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (live) {
-          const float* sp = srow0 + tq[qt] * a.ld + s;
+        const float* sp = srow[qt] + s;
+        float v4[4];
+        if (inner) {
           if (a.vec) {
-            sv = *reinterpret_cast<const float4*>(sp);
-          } else {  // entries past the query are never read: they may lie past the row
-            sv.x = sp[0];
-            sv.y = (s + 1 <= tq[qt]) ? sp[1] : 0.f;
-            sv.z = (s + 2 <= tq[qt]) ? sp[2] : 0.f;
-            sv.w = (s + 3 <= tq[qt]) ? sp[3] : 0.f;
+            const float4 f = *reinterpret_cast<const float4*>(sp);
+            v4[0] = f.x; v4[1] = f.y; v4[2] = f.z; v4[3] = f.w;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v4[r] = sp[r];
           }
+        } else {
+          // entries past the query (or past T) are never read: they may lie past the row
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v4[r] = (s + r <= tq[qt] && tq[qt] < T) ? sp[r] : -__builtin_nanf("");
         }
-        const float v4[4] = {sv.x, sv.y, sv.z, sv.w};
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const bool on = live && (s + r <= tq[qt]) && (v4[r] >= thr[qt]);
-          selbits |= on ? (1u << (16 * qt + 4 * j + r)) : 0u;
+          const bool on = v4[r] >= thr[qt];  // NaN scores and NaN thresholds select nothing
+          bias[qt][j][r] = on ? 0u : 0xffffffffu;
+          any |= on;
         }
       }
     }
-    if (__ballot(selbits != 0u) == 0) continue;  // nothing selected in this wave's 32 x 64 tile
+    if (__ballot(any) == 0) continue;  // nothing selected in this wave's tile
 
     const uint16_t* kl = lds + buf * (KTILE + VTILE);
     const uint16_t* vl = kl + KTILE;
@@ -250,9 +259,12 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
       }
     }
 
-    // Online softmax per query (log2 domain), P^T packed for the second product.
+    // Online softmax per query, log2 domain.  The running max moves only
+    // when a tile's max exceeds it by more than 2^8 (probabilities stay
+    // <= 256, far from overflow in fp32 and exact in scale for 16-bit), so
+    // the O rescale is skipped on almost every tile.
     uint4 pf[2][2];
-    bool rescale = false;
+    bool grow = false;
     float alpha[2];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
@@ -260,24 +272,25 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          mx = fmaxf(mx, ((selbits >> (16 * qt + 4 * j + r)) & 1u) ? st[j][qt][r] * a.scale_log2
-                                                                  : -__builtin_huge_valf());
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[j][qt][r] + __uint_as_float(bias[qt][j][r]));
       mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
       mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-      const float m_new = fmaxf(m[qt], mx);
-      const float m_use = (m_new == -__builtin_huge_valf()) ? 0.f : m_new;
-      alpha[qt] = exp2f(m[qt] - m_use);
-      rescale |= (m_new != m[qt]);
+      const float m_blk = mx * a.scale_log2;
+      const bool up = m_blk > m[qt] + 8.f;
+      const float m_new = up ? m_blk : m[qt];
+      alpha[qt] = up ? exp2f(m[qt] - m_new) : 1.f;   // m = -inf: alpha = 0 on an empty O
+      grow |= up && (m[qt] != -__builtin_huge_valf());
       m[qt] = m_new;
+      const float m_use = (m_new == -__builtin_huge_valf()) ? 0.f : m_new;
       float p[4][4];
       float ps = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          p[j][r] = ((selbits >> (16 * qt + 4 * j + r)) & 1u)
-                        ? exp2f(fmaf(st[j][qt][r], a.scale_log2, -m_use)) : 0.f;
+          const float x = __uint_as_float((bias[qt][j][r] & 0xff800000u) |
+                                          (~bias[qt][j][r] & __float_as_uint(st[j][qt][r])));
+          p[j][r] = __builtin_amdgcn_exp2f(fmaf(x, a.scale_log2, -m_use));  // bare v_exp_f32
           ps += p[j][r];
         }
       l[qt] = fmaf(l[qt], alpha[qt], ps);
@@ -287,7 +300,7 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
                                 M::pack(p[2 * jj + 1][0], p[2 * jj + 1][1]),
                                 M::pack(p[2 * jj + 1][2], p[2 * jj + 1][3]));
     }
-    if (__ballot(rescale) != 0) {
+    if (__ballot(grow) != 0) {
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
