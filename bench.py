@@ -15,6 +15,7 @@ one kernel).  Prints ONE JSON line:
                rows of real config-4 indexer scores): algorithmic bytes
                4*sum(t+1) (+ outputs) / duration, against 8 TB/s
   split        the split forward (indexer, select, attention) at config 1
+  split_c3/c4  the split forward at configs 3 (fp32) and 4 (bf16), per stage
   cpu_baseline the reference's CPU path restated (oracle/, torch-vectorised
                fp32 forward) on the host cores, plus the AVX-512 k-th-largest
                (the reference's own topk_avx512.cpp from oracle/_ref when it
@@ -130,6 +131,53 @@ def bench_split(dev, reps=50):
     for _ in range(5):
         fwd()
     return time_events(fwd, reps, torch.cuda.current_stream(dev))
+
+
+C3 = dict(B=4, T=4096, k=256, HI=8, DI=64, HQ=8, DQ=64, DV=64)
+
+
+def bench_split_long(dev, cfg, dtype, name, reps):
+    """Split forward at a long-row config: indexer (causal half), causal
+    radix-select, attention (the tile kernel where it applies), each stage
+    timed with HIP events on the stream it runs on."""
+    import torch
+
+    from dsa_attention import sparse_attention_hip
+    from lightning_indexer import indexer_scores_hip
+    from topk_threshold import topk_threshold
+
+    B, T, k = cfg["B"], cfg["T"], cfg["k"]
+    ins = gpu_inputs(cfg, dtype, dev, seed=3)
+    stream = torch.cuda.current_stream(dev)
+    scores = torch.empty(B, T, T, device=dev)
+    thr = torch.empty(B, T, 1, device=dev)
+    out = torch.empty(B, T, cfg["HQ"], cfg["DV"], device=dev)
+    ix = lambda: indexer_scores_hip(*ins[:3], write_upper=False, out=scores)  # noqa: E731
+    sel = lambda: thr.copy_(topk_threshold(scores, min(k, T), causal=True))  # noqa: E731
+    att = lambda: sparse_attention_hip(scores, thr, *ins[3:], out=out)  # noqa: E731
+
+    def fwd():
+        ix()
+        sel()
+        att()
+
+    fwd()
+    t_ix = time_events(ix, reps, stream)
+    t_sel = time_events(sel, reps, stream)
+    t_att = time_events(att, reps, stream)
+    t_fwd = time_events(fwd, reps, stream)
+    idx_fl = indexer_flops(B, T, cfg["HI"], cfg["DI"])
+    res = {"workload": f"{name}: split forward B={B},T={T},k={k},HI={cfg['HI']},DI={cfg['DI']},"
+                       f"HQ={cfg['HQ']},DQ=DV={cfg['DQ']} {str(dtype).replace('torch.', '')}",
+           "ms_per_forward": round(t_fwd * 1e3, 4),
+           "query_tokens_per_s": round(B * T / t_fwd, 1),
+           "indexer_ms": round(t_ix * 1e3, 4),
+           "indexer_TFLOP_per_s": round(idx_fl / t_ix / 1e12, 1),
+           "select_ms": round(t_sel * 1e3, 4),
+           "select_GB_per_s": round((4.0 * B * T * (T + 1) / 2 + 4.0 * B * T) / t_sel / 1e9, 1),
+           "attention_ms": round(t_att * 1e3, 4)}
+    del ins, scores, thr, out
+    return res
 
 
 def bench_select_c4(dev, reps=20):
@@ -270,6 +318,8 @@ def main():
     ap.add_argument("--mode", choices=("graph", "eager"), default="graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-select", action="store_true", help="skip the config-4 select leg")
+    ap.add_argument("--no-long", action="store_true",
+                    help="skip the split-forward legs at configs 3 and 4")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run only the workload profiled for HBM traffic: one 256 MiB "
                          "device-to-device copy (counter calibration), then --steps eager "
@@ -328,6 +378,10 @@ def main():
     if not args.no_select:
         log("bench: select at config 4")
         out["topk_select"] = bench_select_c4(dev)
+    if not args.no_long:
+        log("bench: split forward at configs 3 and 4")
+        out["split_c3"] = bench_split_long(dev, C3, torch.float32, "config 3", 10)
+        out["split_c4"] = bench_split_long(dev, C4, torch.bfloat16, "config 4", 5)
     if not args.no_cpu:
         log("bench: CPU baseline")
         out["cpu_baseline"] = cpu_baseline()

@@ -12,8 +12,11 @@
 //
 // Block = 4 waves = 128 consecutive queries of one (batch element, head);
 // wave w owns queries t0+32w .. t0+32w+31 (two 16-query MFMA column tiles).
-// Key tiles of 64 keys are staged in LDS (K as [key][d], V transposed as
-// [d][key]), double-buffered with one barrier per tile.
+// Key tiles of 64 keys are copied HBM -> LDS by the DMA path
+// (global_load_lds_dwordx4: no registers, no LDS store instructions), K and
+// V both as plain [key][d] rows, double-buffered with one barrier per tile.
+// Rows are stored with their 16-byte chunks XOR-swizzled by row so that
+// every LDS read pattern below hits distinct banks.
 //
 // The products are computed transposed, so that no lane exchanges are needed
 // between them (16x16x32 MFMA: A[m][k] lane l holds m = l%16, k-slots
@@ -22,10 +25,14 @@
 //   S^T = K . Q^T   A = K rows (LDS), B = Q^T (registers, loaded once)
 //                   -> lane l: query l%16, keys 4(l/16)+r of each 16-key tile
 //   softmax state (running max m, normaliser l) is per query = per lane
-//   O^T = V^T . P^T A = V^T rows (LDS), B = P^T straight from the S^T
-//                   registers: the 8 k-slots of lane group g are keys
-//                   {4g..4g+3} of key tile 2j and of key tile 2j+1; V^T reads
-//                   use the same key order
+//   O^T = V^T . P^T A = V^T (from the [key][d] V rows by the transposing
+//                   LDS read ds_read_b64_tr_b16: within each 16-lane group,
+//                   lane i's element s is element i%4 of the 8 bytes lane
+//                   4s+i/4 addressed, so lanes addressing rows key0+4g+j/4,
+//                   dims 16dt+4(j%4) receive d = 16dt+i, keys key0+4g+s),
+//                   B = P^T straight from the S^T registers: the 8 k-slots of
+//                   lane group g are keys {4g..4g+3} of key tile 2j and of
+//                   key tile 2j+1
 //                   -> lane l: query l%16, dims 4(l/16)+r of each 16-dim tile
 // P is rounded to the input's 16-bit type for the second product (the
 // reference multiplies fp32 probabilities; the difference is far inside the
@@ -53,7 +60,7 @@ struct TileArgs {
   int HQ;
   float scale_log2;
   float* out;
-  int vec;  // score rows 16-byte aligned with ld % 4 == 0: float4 loads
+  int vec;  // score rows 16-byte aligned with ld % 4 == 0: float4 loads (ld >= 4 then)
 };
 
 template <typename Tag>
@@ -61,7 +68,7 @@ struct Mfma16x16x32;
 
 template <>
 struct Mfma16x16x32<BF16> {
-  static __device__ __forceinline__ f32x4 run(const uint4& a, const uint4& b, f32x4 c) {
+  static __device__ __forceinline__ f32x4 run(const u32x4& a, const u32x4& b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
@@ -74,7 +81,7 @@ struct Mfma16x16x32<BF16> {
 
 template <>
 struct Mfma16x16x32<F16> {
-  static __device__ __forceinline__ f32x4 run(const uint4& a, const uint4& b, f32x4 c) {
+  static __device__ __forceinline__ f32x4 run(const u32x4& a, const u32x4& b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
@@ -85,21 +92,60 @@ struct Mfma16x16x32<F16> {
   }
 };
 
-template <typename Tag, int D>
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+#define DSA_LDS __attribute__((address_space(3)))
+
+// One K or V tile in LDS: 64 rows of D 16-bit elements, 16-byte chunk c of
+// row r stored at chunk position c ^ swz(r).
+template <int D>
+struct TileLds {
+  static constexpr int NCH = D / 8;  // 16-byte chunks per row
+  static constexpr int BYTES = kKT * D * 2;
+  // K is read as 16-byte A fragments by 16 consecutive rows at one chunk:
+  // row % NCH spreads them over NCH chunk positions.
+  static __device__ __forceinline__ int swz_k(int r) { return r & (NCH - 1); }
+  // V is read by the transposing 8-byte reads: 4 consecutive rows at one
+  // chunk pair {2m, 2m+1} per 16-lane group; 2*(r % (NCH/2)) keeps the pair
+  // together and moves it per row.
+  static __device__ __forceinline__ int swz_v(int r) { return (2 * r) & (NCH - 1); }
+};
+
+// Issue this wave's share of the DMA of one tile (rows s0 .. s0+63 of a
+// [T, HQ*D] tensor, this head's D columns) into `dst`.  Rows past T are
+// clamped to T-1 (never causal for any query).  Completion is awaited with
+// vmcnt before the barrier that publishes the tile.
+template <int D, bool IS_K>
+__device__ __forceinline__ void dma_tile(const uint16_t* __restrict__ src, int64_t rowE, int s0,
+                                         int T, DSA_LDS uint8_t* dst, int wave, int lane) {
+  using L = TileLds<D>;
+  constexpr int PER_WAVE = L::BYTES / 1024 / (kNT / kWave);  // 1 KiB DMA instructions per wave
+#pragma unroll
+  for (int i = 0; i < PER_WAVE; ++i) {
+    const int ins = wave * PER_WAVE + i;
+    const int P = ins * 64 + lane;  // physical chunk index this lane fills
+    const int r = P / L::NCH, pc = P % L::NCH;
+    const int lc = pc ^ (IS_K ? L::swz_k(r) : L::swz_v(r));
+    const int s = min(s0 + r, T - 1);
+    __builtin_amdgcn_global_load_lds(src + s * rowE + 8 * lc, dst + ins * 1024, 16, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void wait_dma_and_sync() {
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  block_sync_lds();
+}
+
+template <typename Tag, int D, bool VEC>
 __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
-  static_assert(D % 32 == 0 && D <= 128, "head dim");
+  static_assert(D == 64 || D == 128, "head dim");
   using M = Mfma16x16x32<Tag>;
-  constexpr int KS = D + 8;        // K tile row stride (elements): +16 B keeps b128 reads conflict-free
-  constexpr int VS = kKT + 4;      // V^T tile row stride (elements): +8 B likewise for b64 reads
-  constexpr int KTILE = kKT * KS;  // elements per K tile
-  constexpr int VTILE = D * VS;    // elements per V^T tile
-  constexpr int NKS = D / 32;      // k-steps of the first product
-  constexpr int NDT = D / 16;      // 16-dim output tiles
-  constexpr int PPR = D / 8;       // 16-byte pieces per K/V row
-  constexpr int KCH = kKT * PPR / kNT;        // K pieces per thread per tile
-  constexpr int VCH = (kKT / 2) * PPR / kNT;  // V piece pairs per thread per tile
-  static_assert(KCH >= 1 && VCH >= 1, "tile staging");
-  __shared__ __align__(16) uint16_t lds[2 * (KTILE + VTILE)];
+  using L = TileLds<D>;
+  constexpr int NKS = D / 32;  // k-steps of the first product
+  constexpr int NDT = D / 16;  // 16-dim output tiles
+  // Two buffers per operand, as separate objects: the compiler then knows a
+  // DMA into one buffer does not alias reads of the other, and keeps the
+  // next tile's DMA in flight while the current tile is read.
+  __shared__ __align__(16) uint8_t k0[L::BYTES], k1[L::BYTES], v0[L::BYTES], v1[L::BYTES];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -123,22 +169,30 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
   const uint16_t* Kb = static_cast<const uint16_t*>(a.K) + b * T * rowE + static_cast<int64_t>(h) * D;
   const uint16_t* Vb = static_cast<const uint16_t*>(a.V) + b * T * rowE + static_cast<int64_t>(h) * D;
 
+  const int s_hi = min(T, t0 + kTQ);          // keys [0, s_hi) can be causal in this block
+  const int nkt = (s_hi + kKT - 1) / kKT;
+  const int wave_last = min(tw + 31, T - 1);  // last query of this wave
+
+  DSA_LDS uint8_t* kb[2] = {(DSA_LDS uint8_t*)k0, (DSA_LDS uint8_t*)k1};
+  DSA_LDS uint8_t* vb[2] = {(DSA_LDS uint8_t*)v0, (DSA_LDS uint8_t*)v1};
+  dma_tile<D, true>(Kb, rowE, 0, T, kb[0], wave, lane);
+  dma_tile<D, false>(Vb, rowE, 0, T, vb[0], wave, lane);
+
   // Q^T fragments: qf[qt][ks] = Q[query tw+16qt+c16][dims 32ks+8g .. +8].
-  uint4 qf[2][NKS];
+  u32x4 qf[2][NKS];
   int tq[2];
   float thr[2];
+  const float* srow[2];
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     tq[qt] = tw + 16 * qt + c16;
     const int tl = min(tq[qt], T - 1);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks)
-      qf[qt][ks] = *reinterpret_cast<const uint4*>(Qb + tl * rowE + 32 * ks + 8 * g);
+      qf[qt][ks] = *reinterpret_cast<const u32x4*>(Qb + tl * rowE + 32 * ks + 8 * g);
     thr[qt] = a.thr[b * T + tl];
+    srow[qt] = a.scores + (b * T + tl) * a.ld;
   }
-  const float* srow[2];
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt) srow[qt] = a.scores + (b * T + min(tq[qt], T - 1)) * a.ld;
 
   float m[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()};
   float l[2] = {0.f, 0.f};
@@ -148,104 +202,73 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) o[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int s_hi = min(T, t0 + kTQ);          // keys [0, s_hi) can be causal in this block
-  const int nkt = (s_hi + kKT - 1) / kKT;
-  const int wave_last = min(tw + 31, T - 1);  // last query of this wave
+  // Per-lane LDS read offsets within a tile (the swizzles depend on the row
+  // only through c16 (K) and 4g + c16/4 (V), so they are loop invariant).
+  int kofs[NKS], vofs[NDT];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) kofs[ks] = c16 * (2 * D) + 16 * ((4 * ks + g) ^ L::swz_k(c16));
+  {
+    const int vr = 4 * g + (c16 >> 2);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+      vofs[dt] = vr * (2 * D) + 16 * ((2 * dt + ((c16 & 3) >> 1)) ^ L::swz_v(vr)) + 8 * (c16 & 1);
+  }
 
-  // Global -> registers (prefetch) -> LDS staging of key tile kt.  Rows past
-  // T are clamped to T-1: they are never causal for any query.
-  u32x4 kreg[KCH];  // native vectors: a uint4 struct array here stays in scratch memory
-  u32x4 vreg[VCH][2];
-  auto gload = [&](int kt) {
+  // This wave's scores of key tile kt: sv[qt][j][r] = scores[tq[qt]][s0 +
+  // 16j + 4g + r].  Always the same loads (addresses clamped into the row;
+  // entries that are not causal are masked in compute), with no branches:
+  // loads complete in order, so with a fixed count the mask waits for these
+  // loads only and not for the next tile's DMA issued behind them.
+  const int64_t s_clamp = VEC ? a.ld - 4 : a.ld - 1;
+  auto load_scores = [&](int kt, float (&sv)[2][4][4]) {
     const int s0 = kt * kKT;
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int c = tid + kNT * i;
-      const int s = min(s0 + c / PPR, T - 1);
-      kreg[i] = *reinterpret_cast<const u32x4*>(Kb + s * rowE + 8 * (c % PPR));
-    }
-#pragma unroll
-    for (int i = 0; i < VCH; ++i) {
-      const int c = tid + kNT * i;
-      const int s = s0 + 2 * (c / PPR);
-      vreg[i][0] = *reinterpret_cast<const u32x4*>(Vb + min(s, T - 1) * rowE + 8 * (c % PPR));
-      vreg[i][1] = *reinterpret_cast<const u32x4*>(Vb + min(s + 1, T - 1) * rowE + 8 * (c % PPR));
-    }
-  };
-  auto swrite = [&](int buf) {
-    uint16_t* kl = lds + buf * (KTILE + VTILE);
-    uint16_t* vl = kl + KTILE;
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int c = tid + kNT * i;
-      *reinterpret_cast<u32x4*>(kl + (c / PPR) * KS + 8 * (c % PPR)) = kreg[i];
-    }
-#pragma unroll
-    for (int i = 0; i < VCH; ++i) {
-      const int c = tid + kNT * i;
-      const int kp = c / PPR, d0 = 8 * (c % PPR);
-      const u32x4 w0 = vreg[i][0], w1 = vreg[i][1];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t lo = (w0[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-        const uint32_t hi = (w1[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-        *reinterpret_cast<uint32_t*>(vl + (d0 + e) * VS + 2 * kp) = lo | (hi << 16);
-      }
-    }
-  };
-
-  gload(0);
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int buf = kt & 1;
-    swrite(buf);
-    block_sync_lds();
-    gload(min(kt + 1, nkt - 1));  // unconditional: keeps the prefetch registers out of memory
-    const int s0 = kt * kKT;
-    if (s0 > wave_last) continue;  // the whole tile is above this wave's diagonal
-
-    // Selection of this wave's 32 x 64 tile, as a per-entry bias word:
-    // 0.0f where (query tq[qt], key s0 + 16j + 4g + r) is selected, all-ones
-    // (a NaN) where not.  st + bias is st or NaN, which fmaxf skips, and
-    // v_bfi(bias, -inf, st) is st or -inf: both exact for any st, NaN and
-    // +-inf logits of unselected keys included (the reference masks them to
-    // -inf before its softmax).
-    const bool inner = (s0 + kKT - 1 <= tw) && (tw + 31 < T);  // no causal or row-end test
-    uint32_t bias[2][4][4];
-    bool any = false;
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int s = s0 + 16 * j + 4 * g;
-        const float* sp = srow[qt] + s;
-        float v4[4];
-        if (inner) {
-          if (a.vec) {
-            const float4 f = *reinterpret_cast<const float4*>(sp);
-            v4[0] = f.x; v4[1] = f.y; v4[2] = f.z; v4[3] = f.w;
-          } else {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) v4[r] = sp[r];
-          }
+        if constexpr (VEC) {
+          const float4 f = *reinterpret_cast<const float4*>(srow[qt] + min<int64_t>(s, s_clamp));
+          sv[qt][j][0] = f.x; sv[qt][j][1] = f.y; sv[qt][j][2] = f.z; sv[qt][j][3] = f.w;
         } else {
-          // entries past the query (or past T) are never read: they may lie past the row
 #pragma unroll
-          for (int r = 0; r < 4; ++r) v4[r] = (s + r <= tq[qt] && tq[qt] < T) ? sp[r] : -__builtin_nanf("");
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const bool on = v4[r] >= thr[qt];  // NaN scores and NaN thresholds select nothing
-          bias[qt][j][r] = on ? 0u : 0xffffffffu;
-          any |= on;
+          for (int r = 0; r < 4; ++r) sv[qt][j][r] = srow[qt][min<int64_t>(s + r, s_clamp)];
         }
       }
     }
-    if (__ballot(any) == 0) continue;  // nothing selected in this wave's tile
+  };
 
-    const uint16_t* kl = lds + buf * (KTILE + VTILE);
-    const uint16_t* vl = kl + KTILE;
+  // Selection of this wave's 32 x 64 tile, as a per-entry bias word: 0.0f
+  // where (query tq[qt], key s0 + 16j + 4g + r) is selected, all-ones (a
+  // NaN) where not.  st + bias is st or NaN, which fmaxf skips, and
+  // (bias & -inf) | (~bias & st) is st or -inf: both exact for any st, NaN
+  // and +-inf logits of unselected keys included (the reference masks them
+  // to -inf before its softmax).  Returns whether the wave has work in the
+  // tile.  Bitwise & and | keep it branch-free.
+  auto make_bias = [&](int kt, const float (&sv)[2][4][4], uint32_t (&bias)[2][4][4]) {
+    const int s0 = kt * kKT;
+    const bool inner = (s0 + kKT - 1 <= tw) && (tw + 31 < T);  // every entry causal
+    bool any = false;
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int s = s0 + 16 * j + 4 * g + r;
+          // NaN scores and thresholds select nothing
+          const bool on = (inner | ((s <= tq[qt]) & (tq[qt] < T))) & (sv[qt][j][r] >= thr[qt]);
+          bias[qt][j][r] = on ? 0u : 0xffffffffu;
+          any |= on;
+        }
+    return s0 <= wave_last && __ballot(any) != 0;
+  };
 
-    // S^T = K . Q^T
+  // Everything one wave does with key tile kt, staged in (kl, vl).
+  auto compute = [&](const uint32_t (&bias)[2][4][4], const DSA_LDS uint8_t* kl,
+                     const DSA_LDS uint8_t* vl) {
+    // S^T = K . Q^T; A fragment = K row 16j+c16, chunk 4ks+g (swizzled):
+    // byte offset kofs[ks] + 16j rows (swz_k(16j+c16) = swz_k(c16)).
     f32x4 st[4][2];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -253,7 +276,7 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
       for (int qt = 0; qt < 2; ++qt) st[j][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        const uint4 ka = *reinterpret_cast<const uint4*>(kl + (16 * j + c16) * KS + 32 * ks + 8 * g);
+        const u32x4 ka = *reinterpret_cast<const DSA_LDS u32x4*>(kl + kofs[ks] + 16 * j * (2 * D));
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) st[j][qt] = M::run(ka, qf[qt][ks], st[j][qt]);
       }
@@ -263,7 +286,7 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
     // when a tile's max exceeds it by more than 2^8 (probabilities stay
     // <= 256, far from overflow in fp32 and exact in scale for 16-bit), so
     // the O rescale is skipped on almost every tile.
-    uint4 pf[2][2];
+    u32x4 pf[2][2];
     bool grow = false;
     float alpha[2];
 #pragma unroll
@@ -296,9 +319,9 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
       l[qt] = fmaf(l[qt], alpha[qt], ps);
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj)
-        pf[qt][jj] = make_uint4(M::pack(p[2 * jj][0], p[2 * jj][1]), M::pack(p[2 * jj][2], p[2 * jj][3]),
-                                M::pack(p[2 * jj + 1][0], p[2 * jj + 1][1]),
-                                M::pack(p[2 * jj + 1][2], p[2 * jj + 1][3]));
+        pf[qt][jj] = u32x4{M::pack(p[2 * jj][0], p[2 * jj][1]), M::pack(p[2 * jj][2], p[2 * jj][3]),
+                           M::pack(p[2 * jj + 1][0], p[2 * jj + 1][1]),
+                           M::pack(p[2 * jj + 1][2], p[2 * jj + 1][3])};
     }
     if (__ballot(grow) != 0) {
 #pragma unroll
@@ -309,19 +332,48 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
           for (int r = 0; r < 4; ++r) o[dt][qt][r] *= alpha[qt];
     }
 
-    // O^T += V^T . P^T
+    // O^T += V^T . P^T.  Lane (g, j=c16) addresses V row key0 + 4g + j/4,
+    // dims 16dt + 4(j%4) .. +3; rows key0 + 16 and + 32 keep the swizzle, so
+    // byte offset vofs[dt] + (32jj + 16h) rows.
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
-        const uint16_t* vr = vl + (16 * dt + c16) * VS + 32 * jj + 4 * g;
-        const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
-        const uint4 va = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        const DSA_LDS uint8_t* va = vl + vofs[dt] + 32 * jj * (2 * D);
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((DSA_LDS s16x4*)va);
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((DSA_LDS s16x4*)(va + 16 * (2 * D)));
+        const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+        const u32x4 vfrag = u32x4{l2.x, l2.y, h2.x, h2.y};
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) o[dt][qt] = M::run(va, pf[qt][jj], o[dt][qt]);
+        for (int qt = 0; qt < 2; ++qt) o[dt][qt] = M::run(vfrag, pf[qt][jj], o[dt][qt]);
       }
     }
+  };
+
+  // Per tile: scores -> mask (waits for the score loads), then the next
+  // tile's DMA is issued (so nothing below waits for it), then the products.
+  wait_dma_and_sync();
+  float sv[2][4][4];
+  uint32_t bias[2][4][4];
+  for (int kt = 0; kt < nkt; kt += 2) {
+    // tile kt in buffers 0 (DMA'd before the barrier above); tile kt+1 -> buffers 1
+    load_scores(kt, sv);
+    bool act = make_bias(kt, sv, bias);
+    if (kt + 1 < nkt) {
+      dma_tile<D, true>(Kb, rowE, (kt + 1) * kKT, T, kb[1], wave, lane);
+      dma_tile<D, false>(Vb, rowE, (kt + 1) * kKT, T, vb[1], wave, lane);
+    }
+    if (act) compute(bias, kb[0], vb[0]);
+    wait_dma_and_sync();
+    if (kt + 1 >= nkt) break;
+    load_scores(kt + 1, sv);
+    act = make_bias(kt + 1, sv, bias);
+    if (kt + 2 < nkt) {
+      dma_tile<D, true>(Kb, rowE, (kt + 2) * kKT, T, kb[0], wave, lane);
+      dma_tile<D, false>(Vb, rowE, (kt + 2) * kKT, T, vb[0], wave, lane);
+    }
+    if (act) compute(bias, kb[1], vb[1]);
+    wait_dma_and_sync();
   }
 
   // O = O^T / l, lane l: query tq[qt], dims 16dt + 4g .. +3.
@@ -346,8 +398,12 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
 template <typename Tag, int D>
 hipError_t launch(const TileArgs& a, hipStream_t stream) {
   const int64_t nblk = a.B * a.HQ * ((a.T + kTQ - 1) / kTQ);
-  hipLaunchKernelGGL((tile_attn_kernel<Tag, D>), dim3(static_cast<unsigned>(nblk)), dim3(kNT), 0,
-                     stream, a);
+  if (a.vec)
+    hipLaunchKernelGGL((tile_attn_kernel<Tag, D, true>), dim3(static_cast<unsigned>(nblk)),
+                       dim3(kNT), 0, stream, a);
+  else
+    hipLaunchKernelGGL((tile_attn_kernel<Tag, D, false>), dim3(static_cast<unsigned>(nblk)),
+                       dim3(kNT), 0, stream, a);
   return hipGetLastError();
 }
 
