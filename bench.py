@@ -9,8 +9,9 @@ one kernel).  Prints ONE JSON line:
 
   value        query tokens/s over the K timed steps (B*T*K / seconds)
   roofline     the fused kernel: algorithmic fp32 FLOPs per launch / its
-               average duration (HIP events around every launch on the stream
-               it runs on), against the fp32 MFMA peak (157.3 TFLOP/s)
+               average duration (HIP events on the stream it runs on, around
+               the K back-to-back launches of the graph), against the fp32
+               MFMA peak (157.3 TFLOP/s)
   topk_select  the radix-select at config 4's shape (T=16384, k=2048, causal
                rows of real config-4 indexer scores): algorithmic bytes
                4*sum(t+1) (+ outputs) / duration, against 8 TB/s
@@ -71,17 +72,20 @@ def gpu_inputs(cfg, dtype, dev, seed=0):
 
 
 def time_events(fn, reps, stream):
-    """Mean duration (s) of fn() over reps, HIP events around each call."""
+    """Mean duration (s) of fn() over reps back-to-back calls: HIP events on
+    `stream` (the stream the kernels are launched on) around the batch, so
+    the host-side launch path overlaps the GPU work and the figure is the
+    kernels' average duration."""
     import torch
 
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(reps)]
-    for a, b in evs:
-        a.record(stream)
-        fn()
-        b.record(stream)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    return sum(a.elapsed_time(b) for a, b in evs) / reps / 1e3
+    a.record(stream)
+    for _ in range(reps):
+        fn()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps / 1e3
 
 
 def bench_fused(args, dev):
@@ -97,9 +101,6 @@ def bench_fused(args, dev):
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
 
-    # Per-launch HIP events: the kernel's average duration.
-    kern_s = time_events(fwd, max(20, min(args.steps, 200)), stream)
-
     if args.mode == "graph":
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
@@ -107,11 +108,21 @@ def bench_fused(args, dev):
                 fwd()
         graph.replay()                 # warm the graph once (untimed)
         torch.cuda.synchronize()
+        # HIP events on the stream the graph's kernels run on: K back-to-back
+        # launches, so elapsed / K is the kernel's average launch duration.
+        stream = torch.cuda.current_stream(dev)
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record(stream)
+        graph.replay()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        kern_s = ev0.elapsed_time(ev1) / 1e3 / args.steps
         t0 = time.perf_counter()
         graph.replay()
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
     else:
+        kern_s = time_events(fwd, max(20, min(args.steps, 200)), stream)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(args.steps):

@@ -17,6 +17,9 @@
 //           (one LDS atomic per wave) and passes 2-3 touch only them;
 //   pass 2  key[20:10] of the keys in the chosen digit;
 //   pass 3  key[9:0].
+// When only thresholds are asked for, the candidates go to one wave instead
+// (wave_select_cand: 8-bit passes with wave-level syncs only) and the other
+// waves of the block exit, freeing their registers for the next rows.
 // A digit holding a single key ends the search early.  Every barrier orders
 // LDS only, so waves of other resident blocks keep their HBM loads in flight
 // while this block histograms -- blocks are sized (<= 64 VGPRs) so that
@@ -205,6 +208,66 @@ __device__ __forceinline__ void emit_indices(int32_t* out, int64_t nchunks, uint
   }
 }
 
+// k-th largest of n candidate keys in LDS that all share their bits above
+// bit `low` (those bits are `prefix`), by one wave: MSD passes over at most 8
+// of the remaining bits, each a 256-bin histogram in `hist` (wave-private
+// LDS) built with ds_add and a wave suffix scan -- wave-level syncs only, no
+// block barrier.  A digit holding a single key ends the search early.
+__device__ __forceinline__ uint32_t wave_select_cand(const uint32_t* cand, uint32_t n,
+                                                     uint32_t prefix, int low, uint32_t krem,
+                                                     uint32_t* hist) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int shift = low;
+  while (shift > 0) {
+    const int bits = shift >= 8 ? 8 : shift;
+    shift -= bits;
+    const uint32_t mask = (1u << bits) - 1u;
+    const int hi = shift + bits;  // may be 32: 64-bit shifts below
+    reinterpret_cast<uint4*>(hist)[lane] = make_uint4(0u, 0u, 0u, 0u);
+    wave_lds_sync();
+    for (uint32_t i = lane; i < n; i += kWave) {
+      const uint32_t kk = cand[i];
+      if ((static_cast<uint64_t>(kk) >> hi) == prefix) atomicAdd(&hist[(kk >> shift) & mask], 1u);
+    }
+    wave_lds_sync();
+    const uint4 h4 = reinterpret_cast<const uint4*>(hist)[lane];
+    const uint32_t h[4] = {h4.x, h4.y, h4.z, h4.w};
+    const uint32_t local = h[0] + h[1] + h[2] + h[3];
+    const uint32_t incl = wave_inclusive_sum(local);
+    const uint32_t total = wave_read_lane(incl, kWave - 1);
+    const uint32_t above = total - incl;  // keys in higher lanes' bins
+    const bool mine = above < krem && above + local >= krem;
+    uint32_t digit = 0, knew = 0, cnt = 0;
+    if (mine) {
+      uint32_t cum = above;
+#pragma unroll
+      for (int i = 3; i >= 0; --i) {
+        if (cnt == 0u && cum + h[i] >= krem) {
+          digit = 4u * lane + i;
+          knew = krem - cum;
+          cnt = h[i];
+        }
+        cum += h[i];
+      }
+    }
+    const int src = __ffsll(static_cast<unsigned long long>(__ballot(mine))) - 1;
+    prefix = (prefix << bits) | wave_read_lane(digit, src);
+    krem = wave_read_lane(knew, src);
+    cnt = wave_read_lane(cnt, src);
+    wave_lds_sync();  // histogram reads done before the next pass clears it
+    if (shift > 0 && cnt == 1u) {
+      uint32_t hit = 0;
+      for (uint32_t i = lane; i < n; i += kWave) {
+        const uint32_t kk = cand[i];
+        if ((kk >> shift) == prefix) hit = kk;
+      }
+      const uint64_t m = __ballot(hit != 0u);
+      return wave_read_lane(hit, __ffsll(static_cast<unsigned long long>(m)) - 1);
+    }
+  }
+  return prefix;
+}
+
 template <bool VEC>
 __device__ __forceinline__ void load_keys4(const float* __restrict__ src, int64_t pos,
                                            int64_t nvalid, uint32_t (&kk)[4]) {
@@ -297,6 +360,14 @@ __global__ __launch_bounds__(NT) void topk_reg_kernel(SelectArgs a) {
       });
       block_sync_lds();
       const uint32_t n_c = cnt;
+      if (a.idx == nullptr) {
+        // Threshold only: one wave finishes on the candidates; the other
+        // waves exit now, so their registers take the next rows' loads.
+        if (tid >= kWave) return;
+        const uint32_t tk = wave_select_cand(cand, n_c, prefix, S1, krem, hist);
+        if (tid == 0) a.thr[row] = key_to_float(tk);
+        return;
+      }
       auto visit_cand = [&](auto&& f) {
         for (uint32_t i = tid; i < n_c; i += NT) f(cand[i]);
       };
