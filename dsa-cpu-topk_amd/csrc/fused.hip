@@ -1,14 +1,18 @@
 // fused.hip -- whole DSA forward in one kernel for T <= 2048 (gfx950).
 //
 // Replaces _dsa_fused_kernel + dsa_attention_triton (reference
-// dsa_attention.py:96-227).  Per wave, for its 4 queries:
-//   1. lightning indexer on MFMA over keys [0, t0+4)  -> score rows in LDS
-//   2. per row, radix-select the k_eff-th largest (wave_select.h)
-//   3. per row, sparse attention over keys with score >= thr (attn_tile.h)
-// The score rows never touch HBM.  The 4 waves of a block hold 16
-// consecutive queries and share nothing but L1, so there is no block barrier;
-// blocks run longest queries first, spread evenly over the XCDs
-// (causal_block_tile).
+// dsa_attention.py:96-227).  A block of 8 waves owns 16 consecutive queries:
+//   1. lightning indexer on MFMA: wave w computes the score rows of queries
+//      t0+4(w%4) .. +3 over one half (w/4) of their causal key range, into
+//      LDS rows shared by the block;
+//   -- one block barrier --
+//   2. wave w takes rows 2w and 2w+1: radix-select of the k_eff-th largest
+//      (wave_select.h), then sparse attention over keys with score >= thr
+//      (attn_tile.h).
+// The score rows never touch HBM.  Splitting the indexer's key range over
+// wave pairs and giving each wave two rows (not four) doubles the waves that
+// hide the gathers' memory latency, at the same MFMA work.  Blocks run
+// longest queries first, spread evenly over the XCDs (causal_block_tile).
 //
 // LDS per block: 16 score rows of RS floats, RS = round_up(T,32) + 16 (the
 // +16 puts consecutive rows on different banks for the MFMA epilogue
@@ -38,12 +42,14 @@ struct FusedArgs {
 };
 
 int row_stride(int T) { return ((T + 31) / 32) * 32 + 16; }
+constexpr int kFusedWaves = 8;
 size_t fused_lds_bytes(int T) {
-  return static_cast<size_t>(16) * row_stride(T) * 4 + 4 * 256 * 4 + 4 * kListCap * 4;
+  return static_cast<size_t>(16) * row_stride(T) * 4 + kFusedWaves * 256 * 4 +
+         kFusedWaves * kListCap * 4;
 }
 
 template <typename Tag, int DI, int KB, int EK, int EV>
-__global__ __launch_bounds__(256) void fused_kernel(FusedArgs a) {
+__global__ __launch_bounds__(64 * kFusedWaves) void fused_kernel(FusedArgs a) {
   using raw = typename Tag::raw;
   extern __shared__ __align__(16) float smem[];
   const int wave = threadIdx.x >> 6;
@@ -55,27 +61,40 @@ __global__ __launch_bounds__(256) void fused_kernel(FusedArgs a) {
   int64_t b;
   int tile;
   causal_block_tile(blockIdx.x, a.B, tiles, b, tile);
-  const int t0 = tile * 16 + wave * 4;
-  if (t0 >= T) return;
 
-  float* rows = smem + wave * 4 * RS;
+  float* rows = smem;  // 16 score rows
   uint32_t* hist = reinterpret_cast<uint32_t*>(smem + 16 * RS) + wave * 256;
-  int* list = reinterpret_cast<int*>(smem + 16 * RS + 4 * 256) + wave * kListCap;
+  int* list = reinterpret_cast<int*>(smem + 16 * RS + kFusedWaves * 256) + wave * kListCap;
 
   const raw* qi = static_cast<const raw*>(a.qi) + b * T * static_cast<int64_t>(a.HI) * DI;
   const raw* ki = static_cast<const raw*>(a.ki) + b * T * static_cast<int64_t>(DI);
   const raw* wi = static_cast<const raw*>(a.wi) + b * T * static_cast<int64_t>(a.HI);
 
-  // 1. indexer rows t0..t0+3 over keys [0, min(T, t0+4)).
-  const int s_end = (t0 + 4 < T) ? t0 + 4 : T;
-  indexer_rows<Tag, DI, KB>(qi, ki, wi, T, a.HI, t0, 0, s_end, [&](int s0, const float(&sc)[KB]) {
+  // 1. indexer rows tq..tq+3 over keys [0, min(T, tq+4)), split in two
+  //    halves of whole super-blocks between waves w and w+4.
+  {
+    const int quad = wave & 3, half = wave >> 2;
+    const int tq = tile * 16 + quad * 4;
+    if (tq < T) {
+      constexpr int SB = 16 * KB;
+      const int s_end = (tq + 4 < T) ? tq + 4 : T;
+      const int nsb = (s_end + SB - 1) / SB;
+      const int mid = (nsb / 2) * SB;
+      const int s_lo = half == 0 ? 0 : mid;
+      const int s_hi = half == 0 ? (mid < s_end ? mid : s_end) : s_end;
+      float* qrows = rows + quad * 4 * RS;
+      if (s_lo < s_hi)
+        indexer_rows<Tag, DI, KB>(qi, ki, wi, T, a.HI, tq, s_lo, s_hi,
+                                  [&](int s0, const float(&sc)[KB]) {
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      const int s = s0 + 16 * kb + r16;
-      if (s < T) rows[g * RS + s] = sc[kb];
+          for (int kb = 0; kb < KB; ++kb) {
+            const int s = s0 + 16 * kb + r16;
+            if (s < T) qrows[g * RS + s] = sc[kb];
+          }
+        });
     }
-  });
-  wave_lds_sync();
+  }
+  block_sync_lds();
 
   const int64_t EQ = static_cast<int64_t>(a.HQ) * a.DQ;
   const int64_t EVt = static_cast<int64_t>(a.HQ) * a.DV;
@@ -83,15 +102,17 @@ __global__ __launch_bounds__(256) void fused_kernel(FusedArgs a) {
   const raw* K = static_cast<const raw*>(a.K) + b * T * EQ;
   const raw* V = static_cast<const raw*>(a.V) + b * T * EVt;
 
-  for (int r = 0; r < 4; ++r) {
-    const int t = t0 + r;
+  // 2. rows 2w, 2w+1 of the block.
+  for (int rr = 0; rr < 2; ++rr) {
+    const int r = 2 * wave + rr;
+    const int t = tile * 16 + r;
     if (t >= T) break;
     const float* row = rows + r * RS;
-    // 2. threshold: k_eff-th largest of the full row, whose s > t entries
-    //    are -inf (dsa_attention.py:41-44).
+    // threshold: k_eff-th largest of the full row, whose s > t entries are
+    // -inf (dsa_attention.py:41-44).
     const int n = t + 1;
     const float thr = (n < a.keff) ? -__builtin_huge_valf() : wave_select_kth(row, n, a.keff, hist);
-    // 3. attention over keys with score >= thr.
+    // attention over keys with score >= thr.
     attend_query<Tag, EK, EV>(
         Q, K, V, t, a.HQ, a.DQ, a.DV, a.scale_log2, thr,
         [&](int s, float(&sv)[4]) {
@@ -118,7 +139,8 @@ hipError_t launch(const FusedArgs& a, hipStream_t stream) {
   }();
   (void)attr_set;
   const int64_t nblk = a.B * ((a.T + 15) / 16);
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(nblk)), dim3(256), lds, stream, a);
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(nblk)), dim3(64 * kFusedWaves), lds, stream,
+                     a);
   return hipGetLastError();
 }
 
