@@ -9,7 +9,9 @@
 // only those K/V rows.  Each K (or V) row is HQ*D contiguous elements; lane
 // l owns elements [l*EK, (l+1)*EK) -- one 16-byte-granular contiguous slice,
 // so a row gather is a single coalesced wave load.  Per-head logits are a
-// butterfly over the DQ/EK lanes of the head.  Softmax is online (running
+// butterfly over the DQ/EK lanes of the head, or, when a head spans exactly
+// as many lanes as a gather group has keys, a reduce-scatter that leaves one
+// key's logit per lane (process_rs).  Softmax is online (running
 // max m, normaliser l) in the log2 domain with fp32 state, so the whole
 // selected set is never materialised and any selected count works -- ties at
 // the threshold can select more than k keys (the reference keeps ties).
@@ -114,6 +116,74 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
     m = mnew;
   };
 
+  // Variant for heads spanning exactly U lanes (K and V slices on the same
+  // lanes): a reduce-scatter sums the U partial dot products so that lane j
+  // of a head ends up holding the logit of key j (U-1 shuffles instead of
+  // U*log2(U)); the softmax then takes one exp per lane, and the U
+  // probabilities are broadcast back for the P*V accumulation.  The
+  // per-lane normaliser holds only the lane's own keys until the end.
+  float lpart = 0.f;
+  auto process_rs = [&](const int* ss, int nu) {
+    float kv[U][EK];
+    float vv[U][EV];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t s = ss[u < nu ? u : 0];
+      if (u < nu) {
+        load_cvt<Tag, EK>(K + s * EQ + lane * EK, kv[u]);
+        load_cvt<Tag, EV>(V + s * EVt + lane * EV, vv[u]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EK; ++e) kv[u][e] = 0.f;
+#pragma unroll
+        for (int e = 0; e < EV; ++e) vv[u][e] = 0.f;
+      }
+    }
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < EK; ++e) d = fmaf(q[e], kv[u][e], d);
+      v[u] = d;
+    }
+    // after the step of width w, lane j keeps the half of its keys selected
+    // by bit w of j: lane j ends with key j of the group
+#pragma unroll
+    for (int w = U / 2, cur = U; w >= 1; w >>= 1, cur >>= 1) {
+      const bool up = (lane & w) != 0;
+#pragma unroll
+      for (int i = 0; i < cur / 2; ++i) {
+        const float keep = up ? v[cur / 2 + i] : v[i];
+        const float send = up ? v[i] : v[cur / 2 + i];
+        v[i] = keep + __shfl_xor(send, w, kWave);
+      }
+    }
+    const int j = lane & (U - 1);
+    const float lg = (j < nu) ? v[0] : -__builtin_huge_valf();
+    float mx = lg;
+#pragma unroll
+    for (int w = 1; w < U; w <<= 1) mx = fmaxf(mx, __shfl_xor(mx, w, kWave));
+    const float mnew = fmaxf(m, mx);
+    const float alpha = exp2f(m - mnew);
+    const float p_own = (j < nu) ? __builtin_amdgcn_exp2f(lg - mnew) : 0.f;
+    lpart = fmaf(lpart, alpha, p_own);
+#pragma unroll
+    for (int e = 0; e < EV; ++e) acc[e] *= alpha;
+    const int base = lane & ~(U - 1);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (u < nu) {
+        const float p = __shfl(p_own, base + u, kWave);
+#pragma unroll
+        for (int e = 0; e < EV; ++e) acc[e] = fmaf(p, vv[u][e], acc[e]);
+      }
+    }
+    m = mnew;
+  };
+  // reduce-scatter needs every lane active on both sides (EQ = EVt = 64*E)
+  const bool use_rs = same_map && lphk == U && EK == EV && EQ == kWave * EK && EVt == kWave * EV;
+
   for (int s0 = 0; s0 <= t; s0 += kListCap) {
     // Lane l scans entries s0 + 8l .. s0 + 8l + 7 (two float4).
     const int sb = s0 + 8 * lane;
@@ -143,8 +213,18 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
     for (int c = 0; c < 8; ++c)
       if (keep[c]) list[p++] = sb + c;
     wave_lds_sync();
-    for (int i = 0; i < total; i += U) process(list + i, min(U, total - i));
+    if (use_rs) {
+      for (int i = 0; i < total; i += U) process_rs(list + i, min(U, total - i));
+    } else {
+      for (int i = 0; i < total; i += U) process(list + i, min(U, total - i));
+    }
     wave_lds_sync();
+  }
+  if (use_rs) {
+    float ls = lpart;
+#pragma unroll
+    for (int w = 1; w < U; w <<= 1) ls += __shfl_xor(ls, w, kWave);
+    lsum = ls;
   }
 
   if (vact) {

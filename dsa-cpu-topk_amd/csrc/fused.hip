@@ -48,8 +48,10 @@ size_t fused_lds_bytes(int T) {
          kFusedWaves * kListCap * 4;
 }
 
+// Narrow indexer rows (DI <= 64) ask for 4 waves per SIMD (<= 128 VGPRs): the
+// whole grid of a T = 512 problem is then resident at once.
 template <typename Tag, int DI, int KB, int EK, int EV>
-__global__ __launch_bounds__(64 * kFusedWaves) void fused_kernel(FusedArgs a) {
+__global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kernel(FusedArgs a) {
   using raw = typename Tag::raw;
   extern __shared__ __align__(16) float smem[];
   const int wave = threadIdx.x >> 6;
