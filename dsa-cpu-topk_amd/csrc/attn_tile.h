@@ -60,25 +60,42 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
 
   // Keys gathered per round trip: as many as fit ~64 registers of K+V.
   constexpr int U = (EK + EV <= 4) ? 16 : (EK + EV <= 8) ? 8 : (EK + EV <= 16) ? 4 : 2;
+  // Loads the K/V slices of keys ss[0..U) (entries past nu repeat key ss[0]
+  // and are ignored by the caller): the group's list entries come in with
+  // vector LDS reads, offsets are 32-bit (the host checks T*HQ*D < 2^31) and
+  // shared by K and V when their rows have the same length, and no load is
+  // predicated -- lanes past the row (EQ < 64*EK) read the row's start and
+  // contribute zero through q = 0 / an unstored accumulator.  So the group's
+  // loads issue back to back, one memory round trip per group.
+  const uint32_t koff_l = kact ? static_cast<uint32_t>(lane * EK) : 0u;
+  const uint32_t voff_l = vact ? static_cast<uint32_t>(lane * EV) : 0u;
+  auto load_group = [&](const int* ss, int nu, float (&kv)[U][EK], float (&vv)[U][EV]) {
+    int sidx[U];
+    if constexpr (U % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < U / 4; ++i) {
+        const int4 v4 = reinterpret_cast<const int4*>(ss)[i];
+        sidx[4 * i] = v4.x; sidx[4 * i + 1] = v4.y; sidx[4 * i + 2] = v4.z; sidx[4 * i + 3] = v4.w;
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) sidx[u] = ss[u];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t s = static_cast<uint32_t>(u < nu ? sidx[u] : sidx[0]);
+      const uint32_t rk = s * static_cast<uint32_t>(EQ);
+      const uint32_t rv = (EQ == EVt) ? rk : s * static_cast<uint32_t>(EVt);
+      load_cvt<Tag, EK>(K + (rk + koff_l), kv[u]);
+      load_cvt<Tag, EV>(V + (rv + voff_l), vv[u]);
+    }
+  };
   // Processes keys ss[0..nu) (nu <= U): all their K/V rows are loaded before
   // any is used, so a group costs one memory round trip.
   auto process = [&](const int* ss, int nu) {
     float kv[U][EK];
     float vv[U][EV];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t s = ss[u < nu ? u : 0];
-      if (kact && u < nu) load_cvt<Tag, EK>(K + s * EQ + lane * EK, kv[u]);
-      else {
-#pragma unroll
-        for (int e = 0; e < EK; ++e) kv[u][e] = 0.f;
-      }
-      if (vact && u < nu) load_cvt<Tag, EV>(V + s * EVt + lane * EV, vv[u]);
-      else {
-#pragma unroll
-        for (int e = 0; e < EV; ++e) vv[u][e] = 0.f;
-      }
-    }
+    load_group(ss, nu, kv, vv);
     float lg[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -126,19 +143,7 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
   auto process_rs = [&](const int* ss, int nu) {
     float kv[U][EK];
     float vv[U][EV];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t s = ss[u < nu ? u : 0];
-      if (u < nu) {
-        load_cvt<Tag, EK>(K + s * EQ + lane * EK, kv[u]);
-        load_cvt<Tag, EV>(V + s * EVt + lane * EV, vv[u]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < EK; ++e) kv[u][e] = 0.f;
-#pragma unroll
-        for (int e = 0; e < EV; ++e) vv[u][e] = 0.f;
-      }
-    }
+    load_group(ss, nu, kv, vv);
     float v[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {

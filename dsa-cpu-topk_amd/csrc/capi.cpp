@@ -60,6 +60,9 @@ int check_attn(int dtype, int64_t B, int64_t T, int HQ, int DQ, int DV, const vo
     return fail(DSA_EINVAL, "%s: HQ=%d DQ=%d DV=%d must be powers of 2", who, HQ, DQ, DV);
   if (!dsa::sparse_attn_supported(dtype, HQ, DQ, DV))
     return fail(DSA_EUNSUPPORTED, "%s: no kernel for HQ=%d DQ=%d DV=%d dtype %d", who, HQ, DQ, DV, dtype);
+  // the gathers index one batch element's K/V rows with 32-bit offsets
+  if (T * HQ * static_cast<int64_t>(DQ > DV ? DQ : DV) > kMaxElems)
+    return fail(DSA_EINVAL, "%s: T*HQ*max(DQ,DV) = %lld must be < 2^31", who, (long long)(T * HQ * static_cast<int64_t>(DQ > DV ? DQ : DV)));
   if (B * T == 0) return DSA_OK;
   if (!Q || !K || !V || !out) return fail(DSA_EINVAL, "%s: null pointer", who);
   if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(out))

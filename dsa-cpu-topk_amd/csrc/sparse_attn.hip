@@ -37,7 +37,7 @@ struct AttnArgs {
 template <typename Tag, int EK, int EV>
 __global__ __launch_bounds__(256) void sparse_attn_kernel(AttnArgs a) {
   using raw = typename Tag::raw;
-  __shared__ int lists[4][kListCap];
+  __shared__ __align__(16) int lists[4][kListCap];
   const int wave = threadIdx.x >> 6;
   const int T = a.T;
   const int tiles = (T + 3) >> 2;
