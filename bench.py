@@ -147,7 +147,7 @@ def bench_split(dev, reps=50):
 C3 = dict(B=4, T=4096, k=256, HI=8, DI=64, HQ=8, DQ=64, DV=64)
 
 
-def bench_split_long(dev, cfg, dtype, name, reps):
+def bench_split_long(dev, cfg, dtype, name, reps, fp8_indexer=False):
     """Split forward at a long-row config: indexer (causal half), causal
     radix-select, attention (the tile kernel where it applies), each stage
     timed with HIP events on the stream it runs on."""
@@ -187,6 +187,17 @@ def bench_split_long(dev, cfg, dtype, name, reps):
            "select_ms": round(t_sel * 1e3, 4),
            "select_GB_per_s": round((4.0 * B * T * (T + 1) / 2 + 4.0 * B * T) / t_sel / 1e9, 1),
            "attention_ms": round(t_att * 1e3, 4)}
+    if fp8_indexer:
+        # the same indexer on e4m3 q_idx/k_idx (w fp32): informational, the
+        # split forward above runs the input dtype
+        q8, k8 = (x.to(torch.float8_e4m3fn) for x in ins[:2])
+        w32 = ins[2].float()
+        ix8 = lambda: indexer_scores_hip(q8, k8, w32, write_upper=False, out=scores)  # noqa: E731
+        ix8()
+        t_ix8 = time_events(ix8, reps, stream)
+        res["indexer_fp8_ms"] = round(t_ix8 * 1e3, 4)
+        res["indexer_fp8_TFLOP_per_s"] = round(idx_fl / t_ix8 / 1e12, 1)
+        del q8, k8, w32
     del ins, scores, thr, out
     return res
 
@@ -234,7 +245,7 @@ def bench_select_c4(dev, reps=20):
     return res
 
 
-def cpu_baseline(budget_s=12.0):
+def cpu_baseline(dev=None, budget_s=12.0):
     """The reference's CPU path, restated: torch-vectorised fp32 DSA forward
     (oracle.dsa_forward, acc=float32) on config 1, plus the AVX-512
     k-th-largest on config 1's score matrix."""
@@ -277,9 +288,28 @@ def cpu_baseline(budget_s=12.0):
     while time.perf_counter() - t0 < 3.0 or reps < 30:
         fn()
         reps += 1
-    res["topk_avx512"] = {"kind": kind, "ms": round((time.perf_counter() - t0) / reps * 1e3, 4),
+    topk_ms = (time.perf_counter() - t0) / reps * 1e3
+    res["topk_avx512"] = {"kind": kind, "ms": round(topk_ms, 4),
                           "sample": "config-1 scores [16,512,512], k=32", "cores": cores,
                           "avx512": "avx512f" in native.cpu_flags()}
+    if dev is not None:
+        # The reference's hybrid path (dsa_hybrid.py:46-66) on this host: the
+        # score matrix crosses PCIe to pinned memory, the CPU selects, the
+        # thresholds come back.  Timed here with HIP events around the copies.
+        B, T = C1["B"], C1["T"]
+        s_gpu = scores.to(dev)
+        s_pin = torch.empty(B, T, T, dtype=torch.float32, pin_memory=True)
+        t_pin = torch.empty(B, T, 1, dtype=torch.float32, pin_memory=True)
+        t_gpu = torch.empty(B, T, 1, device=dev)
+        stream = torch.cuda.current_stream(dev)
+        d2h = time_events(lambda: s_pin.copy_(s_gpu, non_blocking=True), 20, stream)
+        h2d = time_events(lambda: t_gpu.copy_(t_pin, non_blocking=True), 20, stream)
+        res["hybrid_pcie"] = {
+            "workload": "config 1: scores [16,512,512] fp32 d2h, CPU k-th largest, thresholds "
+                        "[16,512,1] h2d (the reference's CPU-offload step)",
+            "d2h_ms": round(d2h * 1e3, 4), "cpu_topk_ms": round(topk_ms, 4),
+            "h2d_ms": round(h2d * 1e3, 4),
+            "offload_ms": round(d2h * 1e3 + topk_ms + h2d * 1e3, 4)}
     return res
 
 
@@ -308,7 +338,11 @@ def pmc_workload(args, dev):
     scores = indexer_scores_hip(q, kk, w, write_upper=False)
     del q, kk, w
     for _ in range(3):
-        topk_threshold(scores, C4["k"], causal=True)
+        thr = topk_threshold(scores, C4["k"], causal=True)
+    Q, K, V = gpu_inputs(C4, torch.bfloat16, dev, seed=5)[3:]
+    out = torch.empty(1, C4["T"], C4["HQ"], C4["DV"], device=dev)
+    for _ in range(2):
+        D.sparse_attention_hip(scores, thr, Q, K, V, out=out)   # the tile kernel at this T
     torch.cuda.synchronize()
     log("pmc workload done")
 
@@ -332,9 +366,10 @@ def main():
     ap.add_argument("--no-long", action="store_true",
                     help="skip the split-forward legs at configs 3 and 4")
     ap.add_argument("--pmc-workload", action="store_true",
-                    help="run only the workload profiled for HBM traffic: one 256 MiB "
+                    help="run only the workload profiled with counters: one 256 MiB "
                          "device-to-device copy (counter calibration), then --steps eager "
-                         "fused launches at config 1 and 3 causal selects at config 4")
+                         "fused launches at config 1, the config-4 indexer, 3 causal "
+                         "selects and 2 tile-attention launches at config 4")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build has no "
@@ -392,10 +427,10 @@ def main():
     if not args.no_long:
         log("bench: split forward at configs 3 and 4")
         out["split_c3"] = bench_split_long(dev, C3, torch.float32, "config 3", 10)
-        out["split_c4"] = bench_split_long(dev, C4, torch.bfloat16, "config 4", 5)
+        out["split_c4"] = bench_split_long(dev, C4, torch.bfloat16, "config 4", 5, fp8_indexer=True)
     if not args.no_cpu:
         log("bench: CPU baseline")
-        out["cpu_baseline"] = cpu_baseline()
+        out["cpu_baseline"] = cpu_baseline(dev)
     print(json.dumps(out), flush=True)
 
 

@@ -19,7 +19,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libdsa_amd.so")
 
-DSA_F32, DSA_BF16, DSA_F16 = 0, 1, 2
+DSA_F32, DSA_BF16, DSA_F16, DSA_FP8 = 0, 1, 2, 3
 DSA_OK, DSA_EINVAL, DSA_EUNSUPPORTED, DSA_EHIP = 0, -1, -2, 1
 
 _lib = None
@@ -83,6 +83,8 @@ def dtype_code(t: torch.dtype) -> int:
         return DSA_BF16
     if t == torch.float16:
         return DSA_F16
+    if t == torch.float8_e4m3fn:
+        return DSA_FP8
     raise AssertionError(f"unsupported dtype {t}")
 
 

@@ -37,13 +37,15 @@ constexpr int64_t kMaxElems = (int64_t{1} << 31) - 1;
 
 int check_indexer(const void* q, const void* k, const void* w, int dtype, int64_t B, int64_t T,
                   int HI, int DI, const float* scores, int64_t ld) {
-  if (!dtype_ok(dtype)) return fail(DSA_EINVAL, "indexer: unknown dtype %d", dtype);
+  if (!dtype_ok(dtype) && dtype != DSA_FP8) return fail(DSA_EINVAL, "indexer: unknown dtype %d", dtype);
   if (B < 0 || T < 0) return fail(DSA_EINVAL, "indexer: negative size B=%lld T=%lld", (long long)B, (long long)T);
   if (T > kMaxElems) return fail(DSA_EINVAL, "indexer: T=%lld too large", (long long)T);
   if (HI < 1 || HI > 256) return fail(DSA_EINVAL, "indexer: HI=%d outside [1,256]", HI);
   if (ld < T) return fail(DSA_EINVAL, "indexer: ld=%lld < T=%lld", (long long)ld, (long long)T);
   if (!dsa::indexer_supported(dtype, DI))
-    return fail(DSA_EUNSUPPORTED, "indexer: DI=%d unsupported for dtype %d (fp32: 16..256, 16-bit: 32..256, powers of two)", DI, dtype);
+    return fail(DSA_EUNSUPPORTED, "indexer: DI=%d unsupported for dtype %d (fp32: 16..256, 16-bit: 32..256, fp8: 64..256, powers of two)", DI, dtype);
+  if (dtype == DSA_FP8 && !dsa::indexer_fp8_fits(HI, DI))
+    return fail(DSA_EUNSUPPORTED, "indexer: fp8 q tile of HI=%d DI=%d exceeds LDS (ceil(HI/4)*(16*DI+64) <= 160 KiB)", HI, DI);
   if (B * T == 0) return DSA_OK;
   if (!q || !k || !w || !scores) return fail(DSA_EINVAL, "indexer: null pointer");
   if (!aligned16(q) || !aligned16(k)) return fail(DSA_EINVAL, "indexer: q_idx/k_idx must be 16-byte aligned");
@@ -153,6 +155,7 @@ int dsa_fused_forward(const void* q_idx, const void* k_idx, const void* w_idx, c
   if (T > dsa::kFusedMaxT)
     return fail(DSA_EUNSUPPORTED, "fused: T=%lld > %lld (use the split pipeline)", (long long)T, (long long)dsa::kFusedMaxT);
   if (top_k < 1) return fail(DSA_EINVAL, "fused: top_k must be >= 1 (got %d)", top_k);
+  if (dtype == DSA_FP8) return fail(DSA_EINVAL, "fused: fp8 is an indexer-only dtype");
   int rc = check_indexer(q_idx, k_idx, w_idx, dtype, B, T, HI, DI, out, T);
   if (rc != DSA_OK) return rc;
   rc = check_attn(dtype, B, T, HQ, DQ, DV, Q, K, V, out, "fused");

@@ -20,6 +20,9 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 struct F32 { using raw = float; static constexpr int kBytes = 4; };
 struct BF16 { using raw = uint16_t; static constexpr int kBytes = 2; };
 struct F16 { using raw = uint16_t; static constexpr int kBytes = 2; };
+// OCP FP8 E4M3 (torch.float8_e4m3fn), gfx950's native fp8: the indexer's
+// q/k only (products on the fp8 MFMA, weights and sums fp32).
+struct FP8 { using raw = uint8_t; static constexpr int kBytes = 1; };
 
 __device__ __forceinline__ float to_f32(F32, float x) { return x; }
 __device__ __forceinline__ float to_f32(BF16, uint16_t x) {

@@ -131,6 +131,37 @@ __device__ __forceinline__ f32x4 mfma_chunk(const uint4& a, const Slice<Tag, E>&
   }
 }
 
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+// fp8: chunks c and c+1 of A (a0, a1) against the same chunks of a key
+// block's B slice on v_mfma_f32_16x16x128_f8f6f4 (E4M3 x E4M3, unscaled).  A
+// slice of one chunk (DI = 64) is padded with zeros.
+template <int E>
+__device__ __forceinline__ f32x4 mfma_fp8(const uint4& a0, const uint4& a1,
+                                          const Slice<FP8, E>& b, int c, f32x4 acc) {
+  constexpr int NC = E / 16;
+  const uint4 b0 = b.v[c];
+  const uint4 b1 = (c + 1 < NC) ? b.v[c + 1 < NC ? c + 1 : c] : make_uint4(0u, 0u, 0u, 0u);
+  const i32x8 av = {static_cast<int>(a0.x), static_cast<int>(a0.y), static_cast<int>(a0.z),
+                    static_cast<int>(a0.w), static_cast<int>(a1.x), static_cast<int>(a1.y),
+                    static_cast<int>(a1.z), static_cast<int>(a1.w)};
+  const i32x8 bv = {static_cast<int>(b0.x), static_cast<int>(b0.y), static_cast<int>(b0.z),
+                    static_cast<int>(b0.w), static_cast<int>(b1.x), static_cast<int>(b1.y),
+                    static_cast<int>(b1.z), static_cast<int>(b1.w)};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc, 0, 0, 0, 0, 0, 0);
+}
+
+// The indexer weights w: the input type, except fp32 alongside fp8 q/k.
+template <typename Tag>
+struct WeightT { using raw = typename Tag::raw; static constexpr bool kF32 = Tag::kBytes == 4; };
+template <>
+struct WeightT<FP8> { using raw = float; static constexpr bool kF32 = true; };
+template <typename Tag>
+__device__ __forceinline__ float weight_f32(typename WeightT<Tag>::raw x) {
+  if constexpr (WeightT<Tag>::kF32) return x;
+  else return to_f32(Tag{}, x);
+}
+
 struct QTileShape {
   int nq;   // quads (4 queries) per block
   int nhg;  // head groups of 4 (HI rounded up)
@@ -170,7 +201,8 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
 
   const raw* q = static_cast<const raw*>(a.q) + b * T * static_cast<int64_t>(HI) * DI;
   const raw* k = static_cast<const raw*>(a.k) + b * T * static_cast<int64_t>(DI);
-  const raw* w = static_cast<const raw*>(a.w) + b * T * static_cast<int64_t>(HI);
+  using wraw = typename WeightT<Tag>::raw;
+  const wraw* w = static_cast<const wraw*>(a.w) + b * T * static_cast<int64_t>(HI);
   float* out = a.scores + (b * T) * a.ld;
 
   uint4* qf = lds;
@@ -199,7 +231,7 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
       const int tl = u / hp4;
       const int h = u - tl * hp4;
       const int t = t0 + tl;
-      const float wv = (t < T && h < HI) ? to_f32(Tag{}, w[static_cast<int64_t>(t) * HI + h]) : 0.f;
+      const float wv = (t < T && h < HI) ? weight_f32<Tag>(w[static_cast<int64_t>(t) * HI + h]) : 0.f;
       wf[((tl >> 2) * nhg + (h >> 2)) * 16 + (tl & 3) * 4 + (h & 3)] = wv;
     }
   }
@@ -240,11 +272,22 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
         f32x4 acc[KB];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) acc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (__is_same(Tag, FP8)) {
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-          const uint4 av = qa[((qd * nhg + hg) * NCH + c) * 64];
+          for (int c = 0; c < NCH; c += 2) {
+            const uint4 a0 = qa[((qd * nhg + hg) * NCH + c) * 64];
+            const uint4 a1 = (c + 1 < NCH) ? qa[((qd * nhg + hg) * NCH + (c + 1 < NCH ? c + 1 : c)) * 64]
+                                           : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-          for (int kb = 0; kb < KB; ++kb) acc[kb] = mfma_chunk<Tag, E>(av, bk[kb], c, acc[kb]);
+            for (int kb = 0; kb < KB; ++kb) acc[kb] = mfma_fp8<E>(a0, a1, bk[kb], c, acc[kb]);
+          }
+        } else {
+#pragma unroll
+          for (int c = 0; c < NCH; ++c) {
+            const uint4 av = qa[((qd * nhg + hg) * NCH + c) * 64];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) acc[kb] = mfma_chunk<Tag, E>(av, bk[kb], c, acc[kb]);
+          }
         }
         const float4 wv = wq[(qd * nhg + hg) * 4];
 #pragma unroll
@@ -342,7 +385,8 @@ hipError_t launch(const IndexerArgs& a, hipStream_t stream) {
     case 2: return launch_qtile<Tag, DI, KB, 2>(a, sh, stream);
     case 1: return launch_qtile<Tag, DI, KB, 1>(a, sh, stream);
   }
-  return launch_stream<Tag, DI, KB>(a, stream);
+  if constexpr (__is_same(Tag, FP8)) return hipErrorNotSupported;  // no streaming fp8 kernel
+  else return launch_stream<Tag, DI, KB>(a, stream);
 }
 
 template <typename Tag, int DI, int KB>
@@ -355,7 +399,13 @@ hipError_t launch_stream(const IndexerArgs& a, hipStream_t stream) {
 
 template <typename Tag>
 hipError_t dispatch_di(const IndexerArgs& a, int DI, hipStream_t stream) {
-  if constexpr (Tag::kBytes == 4) {
+  if constexpr (__is_same(Tag, FP8)) {
+    switch (DI) {
+      case 64: return launch<Tag, 64, 4>(a, stream);
+      case 128: return launch<Tag, 128, 4>(a, stream);
+      case 256: return launch<Tag, 256, 2>(a, stream);
+    }
+  } else if constexpr (Tag::kBytes == 4) {
     switch (DI) {
       case 16: return launch<Tag, 16, 4>(a, stream);
       case 32: return launch<Tag, 32, 4>(a, stream);
@@ -379,7 +429,15 @@ hipError_t dispatch_di(const IndexerArgs& a, int DI, hipStream_t stream) {
 bool indexer_supported(int dtype, int DI) {
   if (dtype == 0) return DI == 16 || DI == 32 || DI == 64 || DI == 128 || DI == 256;
   if (dtype == 1 || dtype == 2) return DI == 32 || DI == 64 || DI == 128 || DI == 256;
+  if (dtype == 3) return DI == 64 || DI == 128 || DI == 256;
   return false;
+}
+
+bool indexer_fp8_fits(int HI, int DI) {
+  // one 4-query tile of fp8 q (16 rows of DI bytes per head group) plus its w
+  // fits the LDS budget; fp8 has no streaming kernel to fall back on
+  const int nhg = (HI + 3) / 4;
+  return static_cast<size_t>(nhg) * (16 * DI + 64) <= kQTileLds;
 }
 
 hipError_t launch_indexer(const void* q, const void* k, const void* w, int dtype, int64_t B,
@@ -391,6 +449,7 @@ hipError_t launch_indexer(const void* q, const void* k, const void* w, int dtype
     case 0: return dispatch_di<F32>(a, DI, stream);
     case 1: return dispatch_di<BF16>(a, DI, stream);
     case 2: return dispatch_di<F16>(a, DI, stream);
+    case 3: return dispatch_di<FP8>(a, DI, stream);
   }
   return hipErrorInvalidValue;
 }

@@ -78,6 +78,22 @@ struct Slice<F16, E> : Slice16<F16, E> {
   }
 };
 
+// fp8 slices: E bytes as 16-byte chunks; the MFMA (16x16x128) takes two
+// chunks of A and of B per step (indexer.hip).
+template <int E>
+struct Slice<FP8, E> {
+  static_assert(E % 16 == 0, "fp8 slices are whole 16-byte chunks");
+  uint4 v[E / 16];
+  __device__ __forceinline__ void load(const uint8_t* __restrict__ p) {
+#pragma unroll
+    for (int i = 0; i < E / 16; ++i) v[i] = *reinterpret_cast<const uint4*>(p + 16 * i);
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < E / 16; ++i) v[i] = make_uint4(0u, 0u, 0u, 0u);
+  }
+};
+
 // Computes scores of queries t0..t0+3 (batch row base pointers given) against
 // keys [s_begin, s_end) in super-blocks of 16*KB keys and hands each finished
 // super-block to sink(s0, sc) where lane l holds sc[kb] = score of query

@@ -53,13 +53,23 @@ def indexer_scores_hip(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor, *,
 
     write_upper=False leaves the s > t triangle untouched (the split pipeline
     never reads it).  `out` may be a preallocated [B,T,T] fp32 buffer.
+
+    q and k both torch.float8_e4m3fn select the fp8 MFMA kernel (unscaled
+    E4M3 operands, exact products, fp32 accumulation; w is taken as fp32).
+    The reference has no fp8 path: its kernel upcasts every load to fp32
+    (lightning_indexer.py:81-91), which fp8 inputs match to fp32 rounding.
     """
     L.require_gpu(q, k, w)
     B, T, H, d = q.shape
     assert k.shape == (B, T, d), f"k shape {tuple(k.shape)} != {(B, T, d)}"
     assert w.shape == (B, T, H), f"w shape {tuple(w.shape)} != {(B, T, H)}"
-    dt = L.common_dtype(q, k, w)
-    q, k, w = (L.prep(x, dt) for x in (q, k, w))
+    if q.dtype == torch.float8_e4m3fn and k.dtype == torch.float8_e4m3fn:
+        dt = torch.float8_e4m3fn
+        q, k = L.prep(q, dt), L.prep(k, dt)
+        w = L.prep(w, torch.float32)
+    else:
+        dt = L.common_dtype(q, k, w)
+        q, k, w = (L.prep(x, dt) for x in (q, k, w))
     if out is None:
         out = torch.empty((B, T, T), device=q.device, dtype=torch.float32)
     else:

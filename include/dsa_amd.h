@@ -35,7 +35,11 @@ extern "C" {
  * case: 16-bit inputs feed MFMA with fp32 accumulation (products are exact),
  * fp32 inputs use the fp32 MFMA.  Outputs are always fp32, as the reference's
  * Triton wrappers allocate them (dsa_attention.py:210, :309). */
-enum dsa_dtype { DSA_F32 = 0, DSA_BF16 = 1, DSA_F16 = 2 };
+enum dsa_dtype { DSA_F32 = 0, DSA_BF16 = 1, DSA_F16 = 2,
+                 /* dsa_indexer_scores only: q_idx/k_idx OCP FP8 E4M3
+                  * (torch.float8_e4m3fn, unscaled), w_idx fp32.  Products are
+                  * exact in the fp32 accumulator of the fp8 MFMA. */
+                 DSA_FP8 = 3 };
 
 enum dsa_status {
   DSA_OK = 0,
@@ -59,7 +63,9 @@ const char* dsa_version(void);
  * Replaces: _indexer_score_kernel + indexer_scores_triton,
  *           reference lightning_indexer.py:54-125 (torch form :26-33).
  * Constraints: B,T >= 1; 1 <= HI <= 256; DI in {16,32,64,128,256} (fp32) or
- *              {32,64,128,256} (bf16/fp16); ld >= T.
+ *              {32,64,128,256} (bf16/fp16) or {64,128,256} (fp8, with
+ *              ceil(HI/4) * (16*DI + 64) <= 160 KiB, e.g. HI*DI <= 32768
+ *              for HI a multiple of 4 and DI >= 128); ld >= T.
  */
 int dsa_indexer_scores(const void* q_idx, const void* k_idx, const void* w_idx,
                        int dtype, int64_t B, int64_t T, int HI, int DI,

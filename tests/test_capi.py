@@ -87,6 +87,26 @@ def test_indexer_rejects_bad_arguments():
     assert f(*ok[:4], 0, *ok[5:]) == L.DSA_OK                                          # B = 0
 
 
+def test_fp8_is_indexer_only():
+    """DSA_FP8 (e4m3 q_idx/k_idx, fp32 w) is accepted by the indexer for
+    DI in {64,128,256} while the q tile fits LDS; attention and the fused
+    kernel reject it as an unknown dtype."""
+    f = L.lib().dsa_indexer_scores
+    fp8 = (FAKE, FAKE, FAKE, L.DSA_FP8)
+    assert f(*fp8, 0, 64, 4, 128, FAKE, 64, 1, None) == L.DSA_OK                       # B = 0
+    assert _rc(f, *fp8, 2, 64, 4, 32, FAKE, 64, 1, None)[0] == L.DSA_EUNSUPPORTED      # DI 32
+    assert _rc(f, *fp8, 2, 64, 256, 256, FAKE, 64, 1, None)[0] == L.DSA_EUNSUPPORTED   # LDS
+    assert f(*fp8, 0, 64, 128, 256, FAKE, 64, 1, None) == L.DSA_OK                     # fits
+    assert f(*fp8, 0, 64, 156, 256, FAKE, 64, 1, None) == L.DSA_OK                     # 39 groups
+    assert _rc(f, *fp8, 2, 64, 160, 256, FAKE, 64, 1, None)[0] == L.DSA_EUNSUPPORTED   # 40 groups
+    a = [FAKE, 64, FAKE, FAKE, FAKE, FAKE, L.DSA_FP8, 2, 64, 4, 32, 32, 0.17, FAKE, None]
+    assert _rc(L.lib().dsa_sparse_attn_threshold, *a)[0] == L.DSA_EINVAL
+    assert _rc(L.lib().dsa_sparse_attn_threshold_tiled, *a)[0] == L.DSA_EINVAL
+    a = [FAKE] * 6 + [L.DSA_FP8, 2, 64, 4, 128, 4, 32, 32, 8, 0.17, FAKE, None]
+    rc, msg = _rc(L.lib().dsa_fused_forward, *a)
+    assert rc == L.DSA_EINVAL and "fp8" in msg
+
+
 def test_sparse_attn_rejects_bad_arguments():
     f = L.lib().dsa_sparse_attn_threshold
     base = [FAKE, 64, FAKE, FAKE, FAKE, FAKE, L.DSA_F32, 2, 64, 4, 32, 32, 0.17, FAKE, None]

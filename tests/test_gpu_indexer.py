@@ -117,3 +117,60 @@ def test_topk_mask_consistency(dev):
     mine = torch.zeros(B, T, T, dtype=torch.bool)
     mine.scatter_(-1, torch.from_numpy(O.select_indices(s.cpu().numpy(), 8)).long(), True)
     assert torch.equal(m, mine)
+
+
+# ---------------------------------------------------------------------------
+# fp8 (OCP E4M3) q_idx/k_idx with fp32 w: no reference counterpart (its
+# kernel upcasts every load to fp32, lightning_indexer.py:81-91), so the
+# oracle takes the e4m3 values upcast to float64.  E4M3 x E4M3 products are
+# exact, but the fp8 MFMA's internal sum of its 128 products is not an IEEE
+# fp32 sum (about 13-14 significant bits): measured max errors are 6e-4 to
+# 2e-3 on scores of magnitude ~10, against ~1e-5 for the fp32 path, and
+# reached 0.93 of a 1e-3 bound.  Bound: rtol = atol = 2e-3 (atol scaled with
+# the operands), inside the 2e-2 low-precision bound.
+# ---------------------------------------------------------------------------
+def run_fp8_case(dev, B, T, HI, DI, *, seed0=0, rows=None, qk_scale=1.0):
+    say(f"indexer fp8 B={B} T={T} HI={HI} DI={DI} scale={qk_scale}")
+    q, k, w, *_ = O.make_inputs(B, T, HI, DI, 1, 1, 1, seed0=seed0)
+    q8 = (q * qk_scale).to(torch.float8_e4m3fn)
+    k8 = (k * qk_scale).to(torch.float8_e4m3fn)
+    s = indexer_scores_hip(q8.to(dev), k8.to(dev), w.to(dev))
+    torch.cuda.synchronize()
+    got = s.cpu() if rows is None else s[:, rows].cpu()
+    want = O.indexer_scores(q8, k8, w, rows=rows)
+    ts = torch.arange(T) if rows is None else torch.tensor(rows)
+    causal = torch.arange(T)[None, :] <= ts[:, None]
+    tol = 2e-3 * qk_scale * qk_scale
+    ok, err, excess = close(got[:, causal], want[:, causal], 2e-3, tol)
+    say(f"  max abs err {err:.3g}, worst err/bound {excess:.3g}")
+    assert ok, f"max abs err {err}"
+    assert bool(torch.isneginf(got[:, ~causal]).all()), "off-causal entries must be -inf"
+
+
+@pytest.mark.parametrize("B,T,HI,DI", [(1, 256, 64, 128), (2, 130, 4, 64), (1, 200, 12, 256),
+                                       (3, 77, 5, 64), (16, 512, 4, 64)])
+def test_fp8_shapes(dev, B, T, HI, DI):
+    run_fp8_case(dev, B, T, HI, DI)
+
+
+def test_fp8_subnormal_and_large_operands(dev):
+    """Operands scaled by 2^-8 put much of q/k in E4M3's subnormal range
+    (|x| < 2^-6); scaled by 2^5 they reach the top binades (max 448).  Both
+    must come out as the exact upcast values' products."""
+    run_fp8_case(dev, 1, 96, 8, 128, seed0=3, qk_scale=2.0 ** -8)
+    run_fp8_case(dev, 1, 96, 8, 128, seed0=4, qk_scale=32.0)
+
+
+def test_fp8_c4_shape_sampled_rows(dev):
+    rows = [0, 5, 2047, 2048, 9000, 16383]
+    run_fp8_case(dev, 1, 16384, 64, 128, rows=rows)
+
+
+def test_fp8_wide_rows_unsupported(dev):
+    """fp8 has no register-streaming kernel: q tiles beyond LDS are refused."""
+    from _dsa_lib import DSAUnsupported
+
+    q = torch.zeros(1, 8, 160, 256, device=dev).to(torch.float8_e4m3fn)
+    k = torch.zeros(1, 8, 256, device=dev).to(torch.float8_e4m3fn)
+    with pytest.raises(DSAUnsupported):
+        indexer_scores_hip(q, k, torch.zeros(1, 8, 160, device=dev))
