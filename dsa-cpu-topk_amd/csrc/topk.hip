@@ -291,8 +291,10 @@ __device__ __forceinline__ void load_keys4(const float* __restrict__ src, int64_
 // ---------------------------------------------------------------------------
 // Register-resident kernel: rows up to 4*NT*(V/4) entries; first digit P1 bits.
 // ---------------------------------------------------------------------------
+// Keys plus ~30 working registers fit 64 VGPRs up to V = 32: blocks of up to
+// 512 threads ask for 8 waves per SIMD there, so that four rows share a CU.
 template <int NT, int V, int P1, bool VEC>
-__global__ __launch_bounds__(NT) void topk_reg_kernel(SelectArgs a) {
+__global__ __launch_bounds__(NT, (V <= 32 && NT <= 512) ? 8 : 4) void topk_reg_kernel(SelectArgs a) {
   static_assert(V % 4 == 0 && NT % kWave == 0 && NT <= 1024, "block shape");
   static_assert(P1 == 11 || P1 == 12, "first digit width");
   constexpr int NCH = V / 4;
@@ -320,13 +322,49 @@ __global__ __launch_bounds__(NT) void topk_reg_kernel(SelectArgs a) {
   // chunks that hold any valid entry (block-uniform)
   const int nch = static_cast<int>(min(static_cast<int64_t>(NCH), (nvalid + 4 * NT - 1) / (4 * NT)));
 
+  // All of the row's loads are issued before any is used: one memory round
+  // trip per row.  Addresses are clamped into the row (the last float4, or the
+  // last entry) instead of predicated, so no load sits behind a branch -- a
+  // per-chunk branch made every load wait for the previous one.  Chunks past
+  // nch read that one clamped address and are never visited.
   uint32_t key[V];
+  {
+    const int nv = static_cast<int>(nvalid);  // the host checks n < 2^31
+    // 32-bit byte offsets from the row base (a register row is < 2^30 bytes),
+    // so each load takes one offset register against the scalar base
+    const char* row_bytes = reinterpret_cast<const char*>(src);
+    float raw[V];
+    if constexpr (VEC) {
+      const int last4 = (nv - 1) & ~3;
 #pragma unroll
-  for (int j = 0; j < NCH; ++j) {
-    uint32_t kk[4] = {kKeyNone, kKeyNone, kKeyNone, kKeyNone};
-    if (j < nch) load_keys4<VEC>(src, (static_cast<int64_t>(j) * NT + tid) * 4, nvalid, kk);
+      for (int j = 0; j < NCH; ++j) {
+        const int pos = (j * NT + tid) * 4;
+        const uint32_t off = static_cast<uint32_t>(min(pos, last4)) * 4u;
+        const float4 f = *reinterpret_cast<const float4*>(row_bytes + off);
+        raw[4 * j] = f.x;
+        raw[4 * j + 1] = f.y;
+        raw[4 * j + 2] = f.z;
+        raw[4 * j + 3] = f.w;
+      }
+    } else {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) key[4 * j + c] = kk[c];
+      for (int j = 0; j < NCH; ++j)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const uint32_t off = static_cast<uint32_t>(min((j * NT + tid) * 4 + c, nv - 1)) * 4u;
+          raw[4 * j + c] = *reinterpret_cast<const float*>(row_bytes + off);
+        }
+    }
+    // entries past the row become kKeyNone (0) through a mask, not a branch,
+    // which would let the compiler sink loads into it
+    static_assert(kKeyNone == 0u, "masking assumes kKeyNone == 0");
+#pragma unroll
+    for (int j = 0; j < NCH; ++j)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t valid = ((j * NT + tid) * 4 + c < nv) ? 0xffffffffu : 0u;
+        key[4 * j + c] = float_to_key(raw[4 * j + c]) & valid;
+      }
   }
   auto visit_regs = [&](auto&& f) {
 #pragma unroll
