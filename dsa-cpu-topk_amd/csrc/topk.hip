@@ -140,8 +140,11 @@ __device__ __forceinline__ void find_digit(const uint32_t* hist, uint32_t krem, 
 
 // One radix pass over the keys `visit` enumerates (keys equal to kKeyNone
 // are skipped).  Returns true when the chosen digit holds a single key, whose
-// value is then in thr_key.
-template <int NT, int SHIFT, int BITS, typename Visit>
+// value is then in thr_key.  COUNT_NONE: a first pass (HI = 32) may count
+// kKeyNone (0) into digit 0 instead of testing for it -- no real key has a
+// top digit of 0 (the smallest, -inf, is 0x007fffff), and with at least krem
+// real keys the search never reaches digit 0.
+template <int NT, int SHIFT, int BITS, bool COUNT_NONE = false, typename Visit>
 __device__ __forceinline__ bool radix_pass(Visit&& visit, uint32_t* hist, uint32_t* wsum,
                                            uint32_t* info, uint32_t& prefix, uint32_t& krem,
                                            uint32_t& cnt, bool allow_unique,
@@ -150,9 +153,14 @@ __device__ __forceinline__ bool radix_pass(Visit&& visit, uint32_t* hist, uint32
   constexpr int HI = SHIFT + BITS;
   for (int b = threadIdx.x; b < NB; b += NT) hist[b] = 0u;
   block_sync_lds();
+  static_assert(!COUNT_NONE || HI >= 32, "kKeyNone is in digit 0 only for the first digit");
   visit([&](uint32_t kk) {
-    if (kk != kKeyNone && in_prefix<HI>(kk, prefix))
-      atomicAdd(&hist[(kk >> SHIFT) & (NB - 1)], 1u);
+    if constexpr (COUNT_NONE) {
+      atomicAdd(&hist[kk >> SHIFT], 1u);
+    } else {
+      if (kk != kKeyNone && in_prefix<HI>(kk, prefix))
+        atomicAdd(&hist[(kk >> SHIFT) & (NB - 1)], 1u);
+    }
   });
   block_sync_lds();
   find_digit<NT, NB>(hist, krem, wsum, info);
@@ -355,16 +363,19 @@ __global__ __launch_bounds__(NT, (V <= 32 && NT <= 512) ? 8 : 4) void topk_reg_k
           raw[4 * j + c] = *reinterpret_cast<const float*>(row_bytes + off);
         }
     }
-    // entries past the row become kKeyNone (0) through a mask, not a branch,
-    // which would let the compiler sink loads into it
-    static_assert(kKeyNone == 0u, "masking assumes kKeyNone == 0");
+    // Entries past the row become kKeyNone; only a chunk the row ends inside
+    // needs the per-entry test (block-uniform branch after the conversion,
+    // so no load is sunk into it).
 #pragma unroll
-    for (int j = 0; j < NCH; ++j)
+    for (int j = 0; j < NCH; ++j) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const uint32_t valid = ((j * NT + tid) * 4 + c < nv) ? 0xffffffffu : 0u;
-        key[4 * j + c] = float_to_key(raw[4 * j + c]) & valid;
+      for (int c = 0; c < 4; ++c) key[4 * j + c] = float_to_key(raw[4 * j + c]);
+      if ((j + 1) * NT * 4 > nv) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if ((j * NT + tid) * 4 + c >= nv) key[4 * j + c] = kKeyNone;
       }
+    }
   }
   auto visit_regs = [&](auto&& f) {
 #pragma unroll
@@ -376,10 +387,27 @@ __global__ __launch_bounds__(NT, (V <= 32 && NT <= 512) ? 8 : 4) void topk_reg_k
     }
   };
 
+  // The first pass tests for kKeyNone only in the chunk the row ends inside.
+  auto visit_first = [&](auto&& f) {
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      if (j < nch) {
+        if ((j + 1) * NT * 4 <= nvalid) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) f(key[4 * j + c]);
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (key[4 * j + c] != kKeyNone) f(key[4 * j + c]);
+        }
+      }
+    }
+  };
+
   if (tid == 0) ncand = 0u;
   uint32_t prefix = 0, krem = static_cast<uint32_t>(k), cnt = 0, thr_key = 0;
-  bool found = radix_pass<NT, S1, P1>(visit_regs, hist, wsum, info, prefix, krem, cnt, true,
-                                      thr_key);
+  bool found = radix_pass<NT, S1, P1, true>(visit_first, hist, wsum, info, prefix, krem, cnt,
+                                            true, thr_key);
   if (!found) {
     if (cnt <= static_cast<uint32_t>(kCandCap)) {
       // Compact the chosen digit's keys into LDS: per-lane count, wave scan,
