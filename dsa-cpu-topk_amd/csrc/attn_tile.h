@@ -17,6 +17,9 @@
 // the threshold can select more than k keys (the reference keeps ties).
 #pragma once
 
+#include <type_traits>
+#include <utility>
+
 #include "dsa_device.h"
 
 namespace dsa {
@@ -62,13 +65,18 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
   constexpr int U = (EK + EV <= 4) ? 16 : (EK + EV <= 8) ? 8 : (EK + EV <= 16) ? 4 : 2;
   // Loads the K/V slices of keys ss[0..U) (entries past nu repeat key ss[0]
   // and are ignored by the caller): the group's list entries come in with
-  // vector LDS reads, offsets are 32-bit (the host checks T*HQ*D < 2^31) and
-  // shared by K and V when their rows have the same length, and no load is
-  // predicated -- lanes past the row (EQ < 64*EK) read the row's start and
-  // contribute zero through q = 0 / an unstored accumulator.  So the group's
-  // loads issue back to back, one memory round trip per group.
-  const uint32_t koff_l = kact ? static_cast<uint32_t>(lane * EK) : 0u;
-  const uint32_t voff_l = vact ? static_cast<uint32_t>(lane * EV) : 0u;
+  // vector LDS reads, and every load takes a 32-bit byte offset against the
+  // uniform K or V base (the host keeps a batch element's K and V under
+  // 4 GiB), shared by K and V when their rows have the same length -- one
+  // offset register per key instead of two 64-bit addresses, so all of the
+  // group's loads fit in flight together.  No load is predicated: lanes past
+  // the row (EQ < 64*EK) read the row's start and contribute zero through
+  // q = 0 / an unstored accumulator.  One memory round trip per group.
+  constexpr uint32_t kRaw = sizeof(raw);
+  const uint32_t koff_l = kact ? static_cast<uint32_t>(lane * EK) * kRaw : 0u;
+  const uint32_t voff_l = vact ? static_cast<uint32_t>(lane * EV) * kRaw : 0u;
+  const char* Kb = reinterpret_cast<const char*>(K);
+  const char* Vb = reinterpret_cast<const char*>(V);
   auto load_group = [&](const int* ss, int nu, float (&kv)[U][EK], float (&vv)[U][EV]) {
     int sidx[U];
     if constexpr (U % 4 == 0) {
@@ -84,10 +92,10 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint32_t s = static_cast<uint32_t>(u < nu ? sidx[u] : sidx[0]);
-      const uint32_t rk = s * static_cast<uint32_t>(EQ);
-      const uint32_t rv = (EQ == EVt) ? rk : s * static_cast<uint32_t>(EVt);
-      load_cvt<Tag, EK>(K + (rk + koff_l), kv[u]);
-      load_cvt<Tag, EV>(V + (rv + voff_l), vv[u]);
+      const uint32_t rk = s * (static_cast<uint32_t>(EQ) * kRaw);
+      const uint32_t rv = (EQ == EVt) ? rk : s * (static_cast<uint32_t>(EVt) * kRaw);
+      load_cvt<Tag, EK>(reinterpret_cast<const raw*>(Kb + (rk + koff_l)), kv[u]);
+      load_cvt<Tag, EV>(reinterpret_cast<const raw*>(Vb + (rv + voff_l)), vv[u]);
     }
   };
   // Processes keys ss[0..nu) (nu <= U): all their K/V rows are loaded before
@@ -104,7 +112,20 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
       for (int e = 0; e < EK; ++e) d = fmaf(q[e], kv[u][e], d);
       lg[u] = d;
     }
-    for (int o = 1; o < lphk; o <<= 1) {
+    // sum over the head's lphk lanes: DPP inside 16-lane rows, LDS
+    // permutes across rows
+    auto head_sum = [&](auto step) {
+      constexpr int W = decltype(step)::value;
+      if (lphk > W) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) lg[u] += dpp_partner<W>(lg[u]);
+      }
+    };
+    head_sum(std::integral_constant<int, 1>{});
+    head_sum(std::integral_constant<int, 2>{});
+    head_sum(std::integral_constant<int, 4>{});
+    head_sum(std::integral_constant<int, 8>{});
+    for (int o = 16; o < lphk; o <<= 1) {
 #pragma unroll
       for (int u = 0; u < U; ++u) lg[u] += __shfl_xor(lg[u], o, kWave);
     }
@@ -153,37 +174,51 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
       v[u] = d;
     }
     // after the step of width w, lane j keeps the half of its keys selected
-    // by bit w of j: lane j ends with key j of the group
+    // by bit w of j: lane j ends with key j of the group.  The partner lane
+    // (DPP, inside the row) has the other bit w and the same higher bits.
+    auto rs_step = [&](auto step) {
+      constexpr int W = decltype(step)::value;
+      if constexpr (W < U) {
+        constexpr int cur = 2 * W;
+        const bool up = (lane & W) != 0;
 #pragma unroll
-    for (int w = U / 2, cur = U; w >= 1; w >>= 1, cur >>= 1) {
-      const bool up = (lane & w) != 0;
-#pragma unroll
-      for (int i = 0; i < cur / 2; ++i) {
-        const float keep = up ? v[cur / 2 + i] : v[i];
-        const float send = up ? v[i] : v[cur / 2 + i];
-        v[i] = keep + __shfl_xor(send, w, kWave);
+        for (int i = 0; i < cur / 2; ++i) {
+          const float keep = up ? v[cur / 2 + i] : v[i];
+          const float send = up ? v[i] : v[cur / 2 + i];
+          v[i] = keep + dpp_partner<W>(send);
+        }
       }
-    }
+    };
+    rs_step(std::integral_constant<int, 8>{});
+    rs_step(std::integral_constant<int, 4>{});
+    rs_step(std::integral_constant<int, 2>{});
+    rs_step(std::integral_constant<int, 1>{});
     const int j = lane & (U - 1);
     const float lg = (j < nu) ? v[0] : -__builtin_huge_valf();
     float mx = lg;
-#pragma unroll
-    for (int w = 1; w < U; w <<= 1) mx = fmaxf(mx, __shfl_xor(mx, w, kWave));
+    if constexpr (U > 1) mx = fmaxf(mx, dpp_partner<1>(mx));
+    if constexpr (U > 2) mx = fmaxf(mx, dpp_partner<2>(mx));
+    if constexpr (U > 4) mx = fmaxf(mx, dpp_partner<4>(mx));
+    if constexpr (U > 8) mx = fmaxf(mx, dpp_partner<8>(mx));
     const float mnew = fmaxf(m, mx);
     const float alpha = exp2f(m - mnew);
     const float p_own = (j < nu) ? __builtin_amdgcn_exp2f(lg - mnew) : 0.f;
     lpart = fmaf(lpart, alpha, p_own);
 #pragma unroll
     for (int e = 0; e < EV; ++e) acc[e] *= alpha;
-    const int base = lane & ~(U - 1);
+    auto bcast_acc = [&](auto uc) {
+      constexpr int UU = decltype(uc)::value;
+      if constexpr (UU < U) {
+        if (UU < nu) {
+          const float p = group_bcast<U, UU>(p_own);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (u < nu) {
-        const float p = __shfl(p_own, base + u, kWave);
-#pragma unroll
-        for (int e = 0; e < EV; ++e) acc[e] = fmaf(p, vv[u][e], acc[e]);
+          for (int e = 0; e < EV; ++e) acc[e] = fmaf(p, vv[UU][e], acc[e]);
+        }
       }
-    }
+    };
+    [&]<int... Us>(std::integer_sequence<int, Us...>) {
+      (bcast_acc(std::integral_constant<int, Us>{}), ...);
+    }(std::make_integer_sequence<int, 16>{});
     m = mnew;
   };
   // reduce-scatter needs every lane active on both sides (EQ = EVt = 64*E)
@@ -227,8 +262,10 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
   }
   if (use_rs) {
     float ls = lpart;
-#pragma unroll
-    for (int w = 1; w < U; w <<= 1) ls += __shfl_xor(ls, w, kWave);
+    if constexpr (U > 1) ls += dpp_partner<1>(ls);
+    if constexpr (U > 2) ls += dpp_partner<2>(ls);
+    if constexpr (U > 4) ls += dpp_partner<4>(ls);
+    if constexpr (U > 8) ls += dpp_partner<8>(ls);
     lsum = ls;
   }
 

@@ -40,6 +40,9 @@ int check_indexer(const void* q, const void* k, const void* w, int dtype, int64_
   if (!dtype_ok(dtype) && dtype != DSA_FP8) return fail(DSA_EINVAL, "indexer: unknown dtype %d", dtype);
   if (B < 0 || T < 0) return fail(DSA_EINVAL, "indexer: negative size B=%lld T=%lld", (long long)B, (long long)T);
   if (T > kMaxElems) return fail(DSA_EINVAL, "indexer: T=%lld too large", (long long)T);
+  // the kernels index one batch element's k_idx rows with 32-bit offsets
+  if (T * static_cast<int64_t>(DI > 0 ? DI : 0) > kMaxElems)
+    return fail(DSA_EINVAL, "indexer: T*DI = %lld must be < 2^31", (long long)(T * static_cast<int64_t>(DI)));
   if (HI < 1 || HI > 256) return fail(DSA_EINVAL, "indexer: HI=%d outside [1,256]", HI);
   if (ld < T) return fail(DSA_EINVAL, "indexer: ld=%lld < T=%lld", (long long)ld, (long long)T);
   if (!dsa::indexer_supported(dtype, DI))
@@ -62,9 +65,11 @@ int check_attn(int dtype, int64_t B, int64_t T, int HQ, int DQ, int DV, const vo
     return fail(DSA_EINVAL, "%s: HQ=%d DQ=%d DV=%d must be powers of 2", who, HQ, DQ, DV);
   if (!dsa::sparse_attn_supported(dtype, HQ, DQ, DV))
     return fail(DSA_EUNSUPPORTED, "%s: no kernel for HQ=%d DQ=%d DV=%d dtype %d", who, HQ, DQ, DV, dtype);
-  // the gathers index one batch element's K/V rows with 32-bit offsets
-  if (T * HQ * static_cast<int64_t>(DQ > DV ? DQ : DV) > kMaxElems)
-    return fail(DSA_EINVAL, "%s: T*HQ*max(DQ,DV) = %lld must be < 2^31", who, (long long)(T * HQ * static_cast<int64_t>(DQ > DV ? DQ : DV)));
+  // the gathers address one batch element's K/V rows with 32-bit byte offsets
+  const int64_t esize = dtype == DSA_F32 ? 4 : 2;
+  if (T * HQ * static_cast<int64_t>(DQ > DV ? DQ : DV) * esize > (int64_t{1} << 32) - 1)
+    return fail(DSA_EINVAL, "%s: T*HQ*max(DQ,DV) = %lld elements of %lld bytes must be < 4 GiB", who,
+                (long long)(T * HQ * static_cast<int64_t>(DQ > DV ? DQ : DV)), (long long)esize);
   if (B * T == 0) return DSA_OK;
   if (!Q || !K || !V || !out) return fail(DSA_EINVAL, "%s: null pointer", who);
   if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(out))

@@ -89,6 +89,39 @@ __device__ __forceinline__ T wave_inclusive_sum(T x) {
   return static_cast<T>(v);
 }
 
+// DPP lane moves of a float inside 16-lane rows (VALU, no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// A partner lane for butterfly step W (1, 2, 4 or 8): its bit log2(W)
+// differs from this lane's and its bits above, within the 16-lane row, are
+// the same (mirrors, so the bits below differ too: steps whose data layout
+// depends only on bits already combined do not care).
+template <int W>
+__device__ __forceinline__ float dpp_partner(float v) {
+  static_assert(W == 1 || W == 2 || W == 4 || W == 8, "step inside a row");
+  if constexpr (W == 8) return dpp_f32<0x140>(v);       // row_mirror: i <-> 15-i
+  else if constexpr (W == 4) return dpp_f32<0x141>(v);  // row_half_mirror: i <-> 7-i
+  else if constexpr (W == 2) return dpp_f32<0x1B>(v);   // quad_perm [3,2,1,0]
+  else return dpp_f32<0xB1>(v);                          // quad_perm [1,0,3,2]
+}
+// Lane u of this lane's aligned group of G lanes (G in 2, 4, 8, 16).
+template <int G, int U>
+__device__ __forceinline__ float group_bcast(float v) {
+  static_assert(U >= 0 && U < G, "lane inside the group");
+  if constexpr (G == 16) {
+    return dpp_f32<0x150 + U>(v);  // row_newbcast:U
+  } else if constexpr (G == 8) {
+    const float lo = dpp_f32<0x150 + U>(v), hi = dpp_f32<0x158 + U>(v);
+    return (lane_id() & 8) ? hi : lo;
+  } else if constexpr (G == 4) {
+    return dpp_f32<U | (U << 2) | (U << 4) | (U << 6)>(v);  // quad_perm [U,U,U,U]
+  } else {
+    return dpp_f32<U | (U << 2) | ((U + 2) << 4) | ((U + 2) << 6)>(v);  // [U,U,U+2,U+2]
+  }
+}
+
 // Value of lane `src` (uniform) broadcast to the wave.
 template <typename T>
 __device__ __forceinline__ T wave_read_lane(T x, int src) {
