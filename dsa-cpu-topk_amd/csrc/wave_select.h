@@ -57,10 +57,10 @@ __device__ __forceinline__ float wave_select_kth(const float* row, int n, int k,
       }
     }
     const uint64_t who = __ballot(mine);
-    const int src = __ffsll(static_cast<unsigned long long>(who)) - 1;
-    bucket = __shfl(bucket, src, kWave);
-    knew = __shfl(knew, src, kWave);
-    cnt = __shfl(cnt, src, kWave);
+    const int src = __ffsll(static_cast<unsigned long long>(who)) - 1;  // uniform
+    bucket = wave_read_lane(bucket, src);
+    knew = wave_read_lane(knew, src);
+    cnt = wave_read_lane(cnt, src);
     prefix = (prefix << 8) | bucket;
     krem = knew;
     wave_lds_sync();  // histogram reads done before the next pass clears it
@@ -77,7 +77,7 @@ __device__ __forceinline__ float wave_select_kth(const float* row, int n, int k,
         }
       }
       const uint64_t m = __ballot(hit != 0u);
-      return key_to_float(__shfl(hit, __ffsll(static_cast<unsigned long long>(m)) - 1, kWave));
+      return key_to_float(wave_read_lane(hit, __ffsll(static_cast<unsigned long long>(m)) - 1));
     }
   }
   return key_to_float(prefix);
