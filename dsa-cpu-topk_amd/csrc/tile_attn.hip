@@ -238,14 +238,13 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
     }
   };
 
-  // Selection of this wave's 32 x 64 tile, as a per-entry bias word: 0.0f
-  // where (query tq[qt], key s0 + 16j + 4g + r) is selected, all-ones (a
-  // NaN) where not.  st + bias is st or NaN, which fmaxf skips, and
-  // (bias & -inf) | (~bias & st) is st or -inf: both exact for any st, NaN
-  // and +-inf logits of unselected keys included (the reference masks them
-  // to -inf before its softmax).  Returns whether the wave has work in the
-  // tile.  Bitwise & and | keep it branch-free.
-  auto make_bias = [&](int kt, const float (&sv)[2][4][4], uint32_t (&bias)[2][4][4]) {
+  // Selection of this wave's 32 x 64 tile: sel[qt][j][r] for (query
+  // tq[qt], key s0 + 16j + 4g + r).  Kept as lane masks (one compare each)
+  // and applied once per entry in compute, as a select of the logit or
+  // -inf -- exact for any logit, NaN and +-inf of unselected keys included
+  // (the reference masks them to -inf before its softmax).  Returns whether
+  // the wave has work in the tile.  Bitwise & and | keep it branch-free.
+  auto make_sel = [&](int kt, const float (&sv)[2][4][4], bool (&sel)[2][4][4]) {
     const int s0 = kt * kKT;
     const bool inner = (s0 + kKT - 1 <= tw) && (tw + 31 < T);  // every entry causal
     bool any = false;
@@ -257,15 +256,14 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
         for (int r = 0; r < 4; ++r) {
           const int s = s0 + 16 * j + 4 * g + r;
           // NaN scores and thresholds select nothing
-          const bool on = (inner | ((s <= tq[qt]) & (tq[qt] < T))) & (sv[qt][j][r] >= thr[qt]);
-          bias[qt][j][r] = on ? 0u : 0xffffffffu;
-          any |= on;
+          sel[qt][j][r] = (inner | ((s <= tq[qt]) & (tq[qt] < T))) & (sv[qt][j][r] >= thr[qt]);
+          any |= sel[qt][j][r];
         }
     return s0 <= wave_last && __ballot(any) != 0;
   };
 
   // Everything one wave does with key tile kt, staged in (kl, vl).
-  auto compute = [&](const uint32_t (&bias)[2][4][4], const DSA_LDS uint8_t* kl,
+  auto compute = [&](const bool (&sel)[2][4][4], const DSA_LDS uint8_t* kl,
                      const DSA_LDS uint8_t* vl) {
     // S^T = K . Q^T; A fragment = K row 16j+c16, chunk 4ks+g (swizzled):
     // byte offset kofs[ks] + 16j rows (swz_k(16j+c16) = swz_k(c16)).
@@ -291,11 +289,17 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
     float alpha[2];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
+      // masked logits: the logit where selected, -inf where not
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          st[j][qt][r] = sel[qt][j][r] ? st[j][qt][r] : -__builtin_huge_valf();
       float mx = -__builtin_huge_valf();
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[j][qt][r] + __uint_as_float(bias[qt][j][r]));
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[j][qt][r]);
       mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
       mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
       const float m_blk = mx * a.scale_log2;
@@ -311,9 +315,8 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float x = __uint_as_float((bias[qt][j][r] & 0xff800000u) |
-                                          (~bias[qt][j][r] & __float_as_uint(st[j][qt][r])));
-          p[j][r] = __builtin_amdgcn_exp2f(fmaf(x, a.scale_log2, -m_use));  // bare v_exp_f32
+          // bare v_exp_f32; exp2(-inf) = 0 for unselected keys
+          p[j][r] = __builtin_amdgcn_exp2f(fmaf(st[j][qt][r], a.scale_log2, -m_use));
           ps += p[j][r];
         }
       l[qt] = fmaf(l[qt], alpha[qt], ps);
@@ -354,25 +357,25 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
   // tile's DMA is issued (so nothing below waits for it), then the products.
   wait_dma_and_sync();
   float sv[2][4][4];
-  uint32_t bias[2][4][4];
+  bool sel[2][4][4];
   for (int kt = 0; kt < nkt; kt += 2) {
     // tile kt in buffers 0 (DMA'd before the barrier above); tile kt+1 -> buffers 1
     load_scores(kt, sv);
-    bool act = make_bias(kt, sv, bias);
+    bool act = make_sel(kt, sv, sel);
     if (kt + 1 < nkt) {
       dma_tile<D, true>(Kb, rowE, (kt + 1) * kKT, T, kb[1], wave, lane);
       dma_tile<D, false>(Vb, rowE, (kt + 1) * kKT, T, vb[1], wave, lane);
     }
-    if (act) compute(bias, kb[0], vb[0]);
+    if (act) compute(sel, kb[0], vb[0]);
     wait_dma_and_sync();
     if (kt + 1 >= nkt) break;
     load_scores(kt + 1, sv);
-    act = make_bias(kt + 1, sv, bias);
+    act = make_sel(kt + 1, sv, sel);
     if (kt + 2 < nkt) {
       dma_tile<D, true>(Kb, rowE, (kt + 2) * kKT, T, kb[0], wave, lane);
       dma_tile<D, false>(Vb, rowE, (kt + 2) * kKT, T, vb[0], wave, lane);
     }
-    if (act) compute(bias, kb[1], vb[1]);
+    if (act) compute(sel, kb[1], vb[1]);
     wait_dma_and_sync();
   }
 
