@@ -71,6 +71,21 @@ def gpu_inputs(cfg, dtype, dev, seed=0):
             rn(B, T, HQ, DQ), rn(B, T, HQ, DQ), rn(B, T, HQ, DV))
 
 
+def warm(fn, seconds=0.25):
+    """Run fn() back to back for about `seconds` of wall time before a timed
+    region: the GPU's clocks settle under sustained load (the first tens of
+    milliseconds of a burst run measurably slower)."""
+    import time
+
+    import torch
+
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
+
+
 def time_events(fn, reps, stream):
     """Mean duration (s) of fn() over reps back-to-back calls: HIP events on
     `stream` (the stream the kernels are launched on) around the batch, so
@@ -172,7 +187,7 @@ def bench_split_long(dev, cfg, dtype, name, reps, fp8_indexer=False):
         sel()
         att()
 
-    fwd()
+    warm(fwd)
     t_ix = time_events(ix, reps, stream)
     t_sel = time_events(sel, reps, stream)
     t_att = time_events(att, reps, stream)
@@ -214,8 +229,7 @@ def bench_select_c4(dev, reps=20):
     scores = indexer_scores_hip(*ins[:3], write_upper=False)
     del ins
     stream = torch.cuda.current_stream(dev)
-    for _ in range(3):
-        topk_threshold(scores, k, causal=True)
+    warm(lambda: topk_threshold(scores, k, causal=True))
     t_thr = time_events(lambda: topk_threshold(scores, k, causal=True), reps, stream)
     t_idx = time_events(lambda: topk_indices(scores, k, causal=True), reps, stream)
     read = 4.0 * T * (T + 1) / 2
@@ -234,8 +248,7 @@ def bench_select_c4(dev, reps=20):
     del scores
     # config-2 standalone top-K: [64,2048,2048] N(0,1), k=128
     x = torch.randn((64, 2048, 2048), device=dev, dtype=torch.float32)
-    for _ in range(3):
-        topk_threshold(x, 128)
+    warm(lambda: topk_threshold(x, 128))
     t2 = time_events(lambda: topk_threshold(x, 128), reps, stream)
     b2 = 4.0 * x.numel() + 4.0 * 64 * 2048
     res["c2_standalone"] = {"workload": "[64,2048,2048] N(0,1) fp32, k=128",
