@@ -43,6 +43,7 @@ BASELINE_MS = 5.62             # reference fused Triton forward, README.md:49 (R
 
 C1 = dict(B=16, T=512, k=32, HI=4, DI=32, HQ=4, DQ=32, DV=32)
 C4 = dict(B=1, T=16384, k=2048, HI=64, DI=128, HQ=16, DQ=128, DV=128)
+C2 = dict(B=4, T=512, k=64, HI=4, DI=32, HQ=4, DQ=32, DV=32)  # smallest config-2 batch
 
 
 def log(*a):
@@ -214,6 +215,63 @@ def bench_split_long(dev, cfg, dtype, name, reps, fp8_indexer=False):
         res["indexer_fp8_TFLOP_per_s"] = round(idx_fl / t_ix8 / 1e12, 1)
         del q8, k8, w32
     del ins, scores, thr, out
+    return res
+
+
+def bench_stream(dev, cfg, dtype, name, nbatch=4, reps=3):
+    """Batch streaming (dsa_stream.py): nbatch batches through the split
+    forward one after another, and through the two-stream pipeline that
+    overlaps each batch's indexer with the previous batch's select and
+    attention.  Informational: query tokens/s of each."""
+    import torch
+
+    from dsa_attention import dsa_split_hip
+    from dsa_stream import DSAStreamPipeline
+
+    B, T, k = cfg["B"], cfg["T"], cfg["k"]
+    batches = [gpu_inputs(cfg, dtype, dev, seed=20 + i) for i in range(nbatch)]
+    pipe = DSAStreamPipeline(B, T, k, device=dev)
+
+    def sequential():
+        for bt in batches:
+            dsa_split_hip(*bt, k)
+
+    def streamed():
+        for bt in batches:
+            pipe.submit(*bt)
+        pipe.synchronize()
+
+    import time
+
+    res = {}
+    for leg, fn in (("sequential", sequential), ("streamed", streamed)):
+        warm(fn)
+        best = float("inf")
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            best = min(best, time.perf_counter() - t0)
+        res[leg + "_ms"] = round(best * 1e3, 3)
+        res[leg + "_query_tokens_per_s"] = round(nbatch * B * T / best, 1)
+    # the batches captured once into a HIP graph over static buffers (one stream)
+    from dsa_stream import DSAStreamGraph
+
+    sg = DSAStreamGraph(B, T, cfg["HI"], cfg["DI"], cfg["HQ"], cfg["DQ"], cfg["DV"], k, nbatch,
+                        dtype=dtype, device=dev)
+    for dst, src in zip(sg.inputs, batches):
+        for d_, s_ in zip(dst, src):
+            d_.copy_(s_)
+    warm(sg.replay)
+    stream = torch.cuda.current_stream(dev)
+    t_g = time_events(sg.replay, max(reps, 5), stream)
+    res["graph_ms"] = round(t_g * 1e3, 3)
+    res["graph_query_tokens_per_s"] = round(nbatch * B * T / t_g, 1)
+    res["workload"] = (f"{name} x {nbatch} batches, split forward: one after another (eager), "
+                       "two-stream pipeline (indexer of batch i+1 during select+attention of i), "
+                       "and the batches captured in one HIP graph on one stream")
+    del batches, pipe, sg
     return res
 
 
@@ -441,6 +499,12 @@ def main():
         log("bench: split forward at configs 3 and 4")
         out["split_c3"] = bench_split_long(dev, C3, torch.float32, "config 3", 10)
         out["split_c4"] = bench_split_long(dev, C4, torch.bfloat16, "config 4", 5, fp8_indexer=True)
+        log("bench: batch streaming at configs 2, 3 and 4")
+        out["stream"] = {
+            "c2": bench_stream(dev, C2, torch.float32, "config 2 (B=4,T=512,k=64)", nbatch=16),
+            "c3": bench_stream(dev, C3, torch.float32, "config 3"),
+            "c4": bench_stream(dev, C4, torch.bfloat16, "config 4"),
+        }
     if not args.no_cpu:
         log("bench: CPU baseline")
         out["cpu_baseline"] = cpu_baseline(dev)

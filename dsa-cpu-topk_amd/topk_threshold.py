@@ -37,7 +37,8 @@ def _check(scores: torch.Tensor, k: int) -> int:
     return N
 
 
-def _select(scores: torch.Tensor, k: int, causal: bool, want_idx: bool):
+def _select(scores: torch.Tensor, k: int, causal: bool, want_idx: bool,
+            thr: torch.Tensor | None = None):
     N = _check(scores, k)
     rows = scores.numel() // N if N else 0
     causal_T = 0
@@ -45,7 +46,11 @@ def _select(scores: torch.Tensor, k: int, causal: bool, want_idx: bool):
         if scores.dim() < 2 or scores.shape[-2] != N:
             raise RuntimeError("causal select needs [..., T, T] scores")
         causal_T = N
-    thr = torch.empty(scores.shape[:-1] + (1,), device=scores.device, dtype=torch.float32)
+    if thr is None:
+        thr = torch.empty(scores.shape[:-1] + (1,), device=scores.device, dtype=torch.float32)
+    elif (thr.dtype != torch.float32 or not thr.is_contiguous() or thr.numel() != rows
+          or thr.device != scores.device):
+        raise RuntimeError("thr must be a contiguous fp32 tensor of one value per row")
     idx = None
     if want_idx:
         idx = torch.empty(scores.shape[:-1] + (k,), device=scores.device, dtype=torch.int32)
@@ -67,6 +72,13 @@ def topk_threshold(scores: torch.Tensor, k: int, causal: bool = False) -> torch.
     reference's masked full row holds), halving the bytes read.
     """
     return _select(scores, k, causal, False)[0]
+
+
+def topk_threshold_into(scores: torch.Tensor, k: int, thr: torch.Tensor,
+                        causal: bool = False) -> torch.Tensor:
+    """topk_threshold writing into a preallocated fp32 tensor of one value
+    per row (no allocation: for pipelines that reuse their buffers)."""
+    return _select(scores, k, causal, False, thr)[0]
 
 
 def topk_threshold_batch_merge(scores: torch.Tensor, k: int) -> torch.Tensor:
