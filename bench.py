@@ -275,6 +275,33 @@ def bench_stream(dev, cfg, dtype, name, nbatch=4, reps=3):
     return res
 
 
+def bench_projection(dev, reps=20):
+    """Projection front end (informational): three projection GEMMs + the
+    indexer (the reference's indexer_triton structure) against one fused
+    GEMM read in place by the strided indexer (indexer_from_hidden)."""
+    import torch
+
+    from lightning_indexer import indexer_from_hidden, indexer_scores_hip, project
+
+    res = []
+    for (B, T, D, H, d, dt) in [(2, 96, 128, 4, 64, torch.float32),
+                                (16, 512, 1024, 4, 32, torch.float32),
+                                (1, 4096, 2048, 64, 128, torch.bfloat16)]:
+        g = torch.Generator(device=dev).manual_seed(0)
+        h = torch.randn(B, T, D, generator=g, device=dev).to(dt)
+        Ws = [(torch.randn(D, n, generator=g, device=dev) * 0.03).to(dt) for n in (H * d, d, H)]
+        sep = lambda: indexer_scores_hip(*project(h, *Ws, H, d), write_upper=False)  # noqa: E731
+        fus = lambda: indexer_from_hidden(h, *Ws, H, d, write_upper=False)  # noqa: E731
+        stream = torch.cuda.current_stream(dev)
+        warm(sep, 0.1)
+        t_sep = time_events(sep, reps, stream)
+        warm(fus, 0.1)
+        t_fus = time_events(fus, reps, stream)
+        res.append({"shape": f"B={B},T={T},D={D},HI={H},DI={d},{str(dt).replace('torch.', '')}",
+                    "three_gemms_us": round(t_sep * 1e6, 1), "fused_us": round(t_fus * 1e6, 1)})
+    return res
+
+
 def bench_select_c4(dev, reps=20):
     """Radix-select on config-4 causal rows (real indexer scores)."""
     import torch
@@ -499,6 +526,8 @@ def main():
         log("bench: split forward at configs 3 and 4")
         out["split_c3"] = bench_split_long(dev, C3, torch.float32, "config 3", 10)
         out["split_c4"] = bench_split_long(dev, C4, torch.bfloat16, "config 4", 5, fp8_indexer=True)
+        log("bench: projection front end")
+        out["projection"] = bench_projection(dev)
         log("bench: batch streaming at configs 2, 3 and 4")
         out["stream"] = {
             "c2": bench_stream(dev, C2, torch.float32, "config 2 (B=4,T=512,k=64)", nbatch=16),

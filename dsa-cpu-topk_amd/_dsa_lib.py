@@ -34,6 +34,8 @@ _SIGNATURES = {
     "dsa_version": ([], ctypes.c_char_p),
     "dsa_fused_max_T": ([], _I64),
     "dsa_indexer_scores": ([_P, _P, _P, _I, _I64, _I64, _I, _I, _P, _I64, _I, _P], _I),
+    "dsa_indexer_scores_strided": ([_P, _P, _P, _I, _I64, _I64, _I, _I, _I64, _I64, _I64, _P,
+                                    _I64, _I, _P], _I),
     "dsa_topk_threshold": ([_P, _I64, _I64, _I64, _I, _I64, _P, _P, _P], _I),
     "dsa_sparse_attn_threshold": ([_P, _I64, _P, _P, _P, _P, _I, _I64, _I64, _I, _I, _I, _F,
                                    _P, _P], _I),

@@ -92,9 +92,30 @@ int dsa_indexer_scores(const void* q_idx, const void* k_idx, const void* w_idx, 
                        int write_upper, void* stream) {
   int rc = check_indexer(q_idx, k_idx, w_idx, dtype, B, T, HI, DI, scores, ld);
   if (rc != DSA_OK || B * T == 0) return rc;
-  return hip_status(dsa::launch_indexer(q_idx, k_idx, w_idx, dtype, B, T, HI, DI, scores, ld,
+  return hip_status(dsa::launch_indexer(q_idx, k_idx, w_idx, dtype, B, T, HI, DI,
+                                        static_cast<int64_t>(HI) * DI, DI, HI, scores, ld,
                                         write_upper, static_cast<hipStream_t>(stream)),
                     "dsa_indexer_scores");
+}
+
+int dsa_indexer_scores_strided(const void* q_idx, const void* k_idx, const void* w_idx,
+                               int dtype, int64_t B, int64_t T, int HI, int DI, int64_t ldq,
+                               int64_t ldk, int64_t ldw, float* scores, int64_t ld,
+                               int write_upper, void* stream) {
+  int rc = check_indexer(q_idx, k_idx, w_idx, dtype, B, T, HI, DI, scores, ld);
+  if (rc != DSA_OK) return rc;
+  if (ldq < static_cast<int64_t>(HI) * DI || ldk < DI || ldw < HI)
+    return fail(DSA_EINVAL, "indexer: row strides ldq=%lld ldk=%lld ldw=%lld below HI*DI=%lld, DI=%d, HI=%d",
+                (long long)ldq, (long long)ldk, (long long)ldw, (long long)HI * DI, DI, HI);
+  const int64_t esize = dtype == DSA_F32 ? 4 : dtype == DSA_FP8 ? 1 : 2;
+  if ((ldq * esize) % 16 != 0 || (ldk * esize) % 16 != 0)
+    return fail(DSA_EINVAL, "indexer: ldq and ldk must be multiples of 16 bytes (ldq=%lld ldk=%lld elements)",
+                (long long)ldq, (long long)ldk);
+  if (T * ldk > kMaxElems) return fail(DSA_EINVAL, "indexer: T*ldk must be < 2^31");
+  if (B * T == 0) return DSA_OK;
+  return hip_status(dsa::launch_indexer(q_idx, k_idx, w_idx, dtype, B, T, HI, DI, ldq, ldk, ldw,
+                                        scores, ld, write_upper, static_cast<hipStream_t>(stream)),
+                    "dsa_indexer_scores_strided");
 }
 
 int dsa_topk_threshold(const float* scores, int64_t rows, int64_t n, int64_t ld, int k,

@@ -13,9 +13,11 @@ hipError_t launch_topk(const float* scores, int64_t rows, int64_t n, int64_t ld,
                        int64_t causal_T, float* thr, int32_t* idx, hipStream_t stream);
 
 // Lightning indexer.  dtype: 0 f32, 1 bf16, 2 f16, 3 fp8 e4m3 (w fp32).
+// ldq / ldk / ldw: elements from one token's q / k / w row to the next
+// (HI*DI, DI, HI for packed tensors; a batch element spans T rows).
 hipError_t launch_indexer(const void* q, const void* k, const void* w, int dtype, int64_t B,
-                          int64_t T, int HI, int DI, float* scores, int64_t ld,
-                          int write_upper, hipStream_t stream);
+                          int64_t T, int HI, int DI, int64_t ldq, int64_t ldk, int64_t ldw,
+                          float* scores, int64_t ld, int write_upper, hipStream_t stream);
 bool indexer_supported(int dtype, int DI);
 bool indexer_fp8_fits(int HI, int DI);  // the fp8 kernel's 4-query tile fits LDS
 

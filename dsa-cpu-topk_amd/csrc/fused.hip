@@ -86,7 +86,8 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
       const int s_hi = half == 0 ? (mid < s_end ? mid : s_end) : s_end;
       float* qrows = rows + quad * 4 * RS;
       if (s_lo < s_hi)
-        indexer_rows<Tag, DI, KB>(qi, ki, wi, T, a.HI, tq, s_lo, s_hi,
+        indexer_rows<Tag, DI, KB>(qi, ki, wi, T, a.HI, static_cast<int64_t>(a.HI) * DI, DI,
+                                  a.HI, tq, s_lo, s_hi,
                                   [&](int s0, const float(&sc)[KB]) {
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) {

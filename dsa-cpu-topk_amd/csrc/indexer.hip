@@ -43,6 +43,7 @@ struct IndexerArgs {
   float* scores;
   int64_t ld;
   int write_upper;
+  int64_t ldq, ldk, ldw;  // elements from one token's q / k / w row to the next
 };
 
 template <typename Tag, int DI, int KB>
@@ -61,9 +62,9 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerArgs a) {
   const int c0 = blockIdx.y * kChunk;
   const int c1 = (c0 + kChunk < T) ? c0 + kChunk : T;
 
-  const raw* q = static_cast<const raw*>(a.q) + b * T * static_cast<int64_t>(a.HI) * DI;
-  const raw* k = static_cast<const raw*>(a.k) + b * T * static_cast<int64_t>(DI);
-  const raw* w = static_cast<const raw*>(a.w) + b * T * static_cast<int64_t>(a.HI);
+  const raw* q = static_cast<const raw*>(a.q) + b * T * a.ldq;
+  const raw* k = static_cast<const raw*>(a.k) + b * T * a.ldk;
+  const raw* w = static_cast<const raw*>(a.w) + b * T * a.ldw;
   float* out = a.scores + (b * T) * a.ld;
   const float ninf = -__builtin_huge_valf();
   const int tq = t0 + g;  // this lane's output query
@@ -72,7 +73,8 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerArgs a) {
   const int s_end = (t0 + 4 < c1) ? t0 + 4 : c1;
   int done_end = c0;
   if (s_end > c0) {
-    indexer_rows<Tag, DI, KB>(q, k, w, T, a.HI, t0, c0, s_end, [&](int s0, const float(&sc)[KB]) {
+    indexer_rows<Tag, DI, KB>(q, k, w, T, a.HI, a.ldq, a.ldk, a.ldw, t0, c0, s_end,
+                              [&](int s0, const float(&sc)[KB]) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         const int s = s0 + 16 * kb + r16;
@@ -199,10 +201,10 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
   const int lane = lane_id();
   const int g = lane >> 4, r16 = lane & 15;
 
-  const raw* q = static_cast<const raw*>(a.q) + b * T * static_cast<int64_t>(HI) * DI;
-  const raw* k = static_cast<const raw*>(a.k) + b * T * static_cast<int64_t>(DI);
+  const raw* q = static_cast<const raw*>(a.q) + b * T * a.ldq;
+  const raw* k = static_cast<const raw*>(a.k) + b * T * a.ldk;
   using wraw = typename WeightT<Tag>::raw;
-  const wraw* w = static_cast<const wraw*>(a.w) + b * T * static_cast<int64_t>(HI);
+  const wraw* w = static_cast<const wraw*>(a.w) + b * T * a.ldw;
   float* out = a.scores + (b * T) * a.ld;
 
   uint4* qf = lds;
@@ -221,7 +223,7 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
       const int t = t0 + tl;
       uint4 v = make_uint4(0u, 0u, 0u, 0u);
       if (t < T && h < HI)
-        v = *reinterpret_cast<const uint4*>(q + (static_cast<int64_t>(t) * HI + h) * DI + d0);
+        v = *reinterpret_cast<const uint4*>(q + static_cast<int64_t>(t) * a.ldq + h * DI + d0);
       const int gg = d0 / E;
       const int c = (d0 - gg * E) / EPC;
       const int ln = gg * 16 + 4 * (tl & 3) + (h & 3);
@@ -231,7 +233,7 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
       const int tl = u / hp4;
       const int h = u - tl * hp4;
       const int t = t0 + tl;
-      const float wv = (t < T && h < HI) ? weight_f32<Tag>(w[static_cast<int64_t>(t) * HI + h]) : 0.f;
+      const float wv = (t < T && h < HI) ? weight_f32<Tag>(w[static_cast<int64_t>(t) * a.ldw + h]) : 0.f;
       wf[((tl >> 2) * nhg + (h >> 2)) * 16 + (tl & 3) * 4 + (h & 3)] = wv;
     }
   }
@@ -250,7 +252,7 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
       const int s = min(sbi * SB + 16 * kb + r16, T - 1);
-      bk[kb].load(k + static_cast<int64_t>(s) * DI + g * E);
+      bk[kb].load(k + static_cast<int64_t>(s) * a.ldk + g * E);
     }
   };
 
@@ -441,10 +443,10 @@ bool indexer_fp8_fits(int HI, int DI) {
 }
 
 hipError_t launch_indexer(const void* q, const void* k, const void* w, int dtype, int64_t B,
-                          int64_t T, int HI, int DI, float* scores, int64_t ld,
-                          int write_upper, hipStream_t stream) {
+                          int64_t T, int HI, int DI, int64_t ldq, int64_t ldk, int64_t ldw,
+                          float* scores, int64_t ld, int write_upper, hipStream_t stream) {
   if (B == 0 || T == 0) return hipSuccess;
-  IndexerArgs a{q, k, w, B, static_cast<int>(T), HI, scores, ld, write_upper};
+  IndexerArgs a{q, k, w, B, static_cast<int>(T), HI, scores, ld, write_upper, ldq, ldk, ldw};
   switch (dtype) {
     case 0: return dispatch_di<F32>(a, DI, stream);
     case 1: return dispatch_di<BF16>(a, DI, stream);

@@ -100,13 +100,14 @@ struct Slice<FP8, E> {
 // t0 + l/16 and key s0 + 16*kb + l%16.  Entries with key > query, key >= T or
 // query >= T hold garbage/-inf; the sink applies the causal mask and bounds.
 //
-// q : [T, HI, DI] of this batch element   k : [T, DI]   w : [T, HI]
+// q : [T, HI, DI] of this batch element   k : [T, DI]   w : [T, HI], rows of
+// consecutive tokens ldq / ldk / ldw elements apart.
 template <typename Tag, int DI, int KB, typename Sink>
 __device__ __forceinline__ void indexer_rows(const typename Tag::raw* __restrict__ q,
                                              const typename Tag::raw* __restrict__ k,
                                              const typename Tag::raw* __restrict__ w, int T,
-                                             int HI, int t0, int s_begin, int s_end,
-                                             Sink&& sink) {
+                                             int HI, int64_t ldq, int64_t ldk, int64_t ldw,
+                                             int t0, int s_begin, int s_end, Sink&& sink) {
   constexpr int E = DI / 4;
   using S = Slice<Tag, E>;
   const int lane = lane_id();
@@ -126,13 +127,13 @@ __device__ __forceinline__ void indexer_rows(const typename Tag::raw* __restrict
   auto load_a = [&](int hg, S& a, float (&wv)[4]) {
     const int head = 4 * hg + ha;
     if (qa < T && head < HI)
-      a.load(q + (static_cast<int64_t>(qa) * HI + head) * DI + g * E);
+      a.load(q + static_cast<int64_t>(qa) * ldq + head * DI + g * E);
     else
       a.zero();
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int hw = 4 * hg + r;
-      wv[r] = (qo < T && hw < HI) ? to_f32(Tag{}, w[static_cast<int64_t>(qo) * HI + hw]) : 0.f;
+      wv[r] = (qo < T && hw < HI) ? to_f32(Tag{}, w[static_cast<int64_t>(qo) * ldw + hw]) : 0.f;
     }
   };
   if (nhg == 1) load_a(0, a_cached, w_cached);
@@ -144,7 +145,7 @@ __device__ __forceinline__ void indexer_rows(const typename Tag::raw* __restrict
     for (int kb = 0; kb < KB; ++kb) {
       const int s = s0 + 16 * kb + r16;
       if (s < T)
-        bk[kb].load(k + static_cast<int64_t>(s) * DI + g * E);
+        bk[kb].load(k + static_cast<int64_t>(s) * ldk + g * E);
       else
         bk[kb].zero();
     }

@@ -97,10 +97,60 @@ def indexer_scores_triton(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor,
     return indexer_scores_hip(q, k, w, write_upper=True)
 
 
+_WCAT_CACHE: dict = {}
+
+
+def _fused_weights(W_Q, W_K, W_W, dtype):
+    """[W_Q | W_K | W_W | 0-pad] as one [D, n] matrix, cached per weight
+    tensors (and their in-place versions).  The zero columns pad each row of
+    the projection output to a 16-byte multiple."""
+    key = tuple((W.data_ptr(), W._version, tuple(W.shape)) for W in (W_Q, W_K, W_W)) + (dtype,)
+    wc = _WCAT_CACHE.get(key)
+    if wc is None:
+        D = W_Q.shape[0]
+        n = W_Q.shape[1] + W_K.shape[1] + W_W.shape[1]
+        per16 = 16 // torch.tensor([], dtype=dtype).element_size()
+        n_pad = (n + per16 - 1) // per16 * per16
+        wc = torch.zeros(D, n_pad, device=W_Q.device, dtype=dtype)
+        wc[:, :n].copy_(torch.cat([W_Q, W_K, W_W], dim=1))
+        _WCAT_CACHE.clear()  # keep one entry: weights of the layer in use
+        _WCAT_CACHE[key] = wc
+    return wc
+
+
+def indexer_from_hidden(h, W_Q, W_K, W_W, num_heads, head_dim, *,
+                        write_upper: bool = True) -> torch.Tensor:
+    """Projection front end fused into the indexer's input stage: ONE GEMM
+    h @ [W_Q | W_K | W_W] (hipBLASLt via torch) writes every token's q, k and
+    w side by side, and the MFMA indexer reads them in place through row
+    strides (dsa_indexer_scores_strided) -- no split, no copies.  Same result
+    as project() + indexer_scores_hip (reference lightning_indexer.py:36-47,
+    128-130)."""
+    L.require_gpu(h, W_Q, W_K, W_W)
+    B, T, D = h.shape
+    H, d = num_heads, head_dim
+    assert W_Q.shape == (D, H * d) and W_K.shape == (D, d) and W_W.shape == (D, H), \
+        "projection weight shapes"
+    dt = L.common_dtype(h, W_Q, W_K, W_W)
+    wc = _fused_weights(W_Q, W_K, W_W, dt)
+    y = L.prep(h, dt).reshape(B * T, D) @ wc          # [B*T, n_pad]
+    ldr = y.shape[1]
+    out = torch.empty((B, T, T), device=h.device, dtype=torch.float32)
+    base = y.data_ptr()
+    es = y.element_size()
+    rc = L.lib().dsa_indexer_scores_strided(
+        base, base + H * d * es, base + (H * d + d) * es, L.dtype_code(dt), B, T, H, d,
+        ldr, ldr, ldr, out.data_ptr(), T, 1 if write_upper else 0, L.stream_ptr(h.device))
+    L.check(rc, "indexer_from_hidden")
+    return out
+
+
 def indexer_triton(h, W_Q, W_K, W_W, num_heads, head_dim, **kw):
-    """Projection (hipBLASLt GEMMs via torch) then the MFMA indexer (:128-130)."""
-    q, k, w = project(h, W_Q, W_K, W_W, num_heads, head_dim)
-    return indexer_scores_triton(q, k, w, **kw)
+    """Drop-in for the reference's indexer_triton (:128-130): the projection
+    as one fused GEMM read in place by the MFMA indexer (indexer_from_hidden).
+    BLOCK_T/BLOCK_S keywords are accepted for compatibility."""
+    assert head_dim > 0 and head_dim & (head_dim - 1) == 0, f"head_dim {head_dim} must be power of 2"
+    return indexer_from_hidden(h, W_Q, W_K, W_W, num_heads, head_dim)
 
 
 # ---------------------------------------------------------------------------

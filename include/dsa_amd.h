@@ -73,6 +73,22 @@ int dsa_indexer_scores(const void* q_idx, const void* k_idx, const void* w_idx,
                        void* stream);
 
 /*
+ * dsa_indexer_scores for q_idx / k_idx / w_idx whose consecutive tokens are
+ * ldq / ldk / ldw elements apart (a batch element spans T such rows), e.g.
+ * the three column ranges of one projection GEMM's output [B*T, HI*DI+DI+HI],
+ * read in place.  ldq >= HI*DI, ldk >= DI, ldw >= HI; ldq and ldk (in bytes)
+ * and the q_idx / k_idx pointers 16-byte aligned; T*ldk < 2^31.
+ * No reference counterpart: it fuses the front end of indexer_triton
+ * (reference lightning_indexer.py:128-130, projection :36-47), whose three
+ * separate projections produce packed tensors.
+ */
+int dsa_indexer_scores_strided(const void* q_idx, const void* k_idx, const void* w_idx,
+                               int dtype, int64_t B, int64_t T, int HI, int DI,
+                               int64_t ldq, int64_t ldk, int64_t ldw,
+                               float* scores, int64_t ld, int write_upper,
+                               void* stream);
+
+/*
  * Per-row k-th largest ("top-K threshold") with an optional exactly-k index set.
  *   thr[r] = k-th largest of row r, ties counted (torch.topk(x,k).values[...,-1]).
  *   idx[r*k .. r*k+k) (optional, may be NULL) = the k positions a stable

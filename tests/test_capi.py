@@ -87,6 +87,25 @@ def test_indexer_rejects_bad_arguments():
     assert f(*ok[:4], 0, *ok[5:]) == L.DSA_OK                                          # B = 0
 
 
+def test_indexer_strided_rejects_bad_strides():
+    f = L.lib().dsa_indexer_scores_strided
+    ok = [FAKE, FAKE, FAKE, L.DSA_F32, 2, 64, 4, 32, 132, 132, 132, FAKE, 64, 1, None]
+    a = list(ok); a[4] = 0
+    assert f(*a) == L.DSA_OK                                         # B = 0, strides fine
+    a = list(ok); a[8] = 120
+    assert _rc(f, *a)[0] == L.DSA_EINVAL                             # ldq < HI*DI
+    a = list(ok); a[9] = 16
+    assert _rc(f, *a)[0] == L.DSA_EINVAL                             # ldk < DI
+    a = list(ok); a[10] = 3
+    assert _rc(f, *a)[0] == L.DSA_EINVAL                             # ldw < HI
+    a = list(ok); a[8] = 130
+    rc, msg = _rc(f, *a)
+    assert rc == L.DSA_EINVAL and "16 bytes" in msg                  # ldq not 16-byte multiple
+    a = list(ok); a[3] = L.DSA_BF16; a[8] = a[9] = a[10] = 136
+    a[4] = 0
+    assert f(*a) == L.DSA_OK                                         # 272-byte rows
+
+
 def test_fp8_is_indexer_only():
     """DSA_FP8 (e4m3 q_idx/k_idx, fp32 w) is accepted by the indexer for
     DI in {64,128,256} while the q tile fits LDS; attention and the fused

@@ -174,3 +174,57 @@ def test_fp8_wide_rows_unsupported(dev):
     k = torch.zeros(1, 8, 256, device=dev).to(torch.float8_e4m3fn)
     with pytest.raises(DSAUnsupported):
         indexer_scores_hip(q, k, torch.zeros(1, 8, 160, device=dev))
+
+
+# ---------------------------------------------------------------------------
+# Row-strided inputs and the fused projection front end
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype,B,T,HI,DI,pad", [(torch.float32, 2, 200, 4, 32, 4),
+                                                  (torch.bfloat16, 1, 300, 8, 64, 8),
+                                                  (torch.float32, 1, 96, 64, 256, 12)])
+def test_strided_rows_equal_packed(dev, dtype, B, T, HI, DI, pad):
+    """q, k, w as column ranges of one [B*T, HI*DI+DI+HI+pad] buffer give the
+    packed entry point's scores bit for bit (same kernel, same values).  The
+    last case takes the register-streaming kernel (q rows too wide for LDS)."""
+    import _dsa_lib as L
+
+    say(f"strided indexer {dtype} B={B} T={T} HI={HI} DI={DI}")
+    q, k, w, *_ = O.make_inputs(B, T, HI, DI, 1, 1, 1, dtype=dtype, seed0=9)
+    RS = HI * DI + DI + HI + pad
+    buf = torch.zeros(B * T, RS, dtype=dtype)
+    buf[:, :HI * DI] = q.reshape(B * T, HI * DI)
+    buf[:, HI * DI:HI * DI + DI] = k.reshape(B * T, DI)
+    buf[:, HI * DI + DI:HI * DI + DI + HI] = w.reshape(B * T, HI)
+    buf = buf.to(dev)
+    want = indexer_scores_hip(q.to(dev), k.to(dev), w.to(dev))
+    got = torch.empty(B, T, T, device=dev)
+    es, base = buf.element_size(), buf.data_ptr()
+    rc = L.lib().dsa_indexer_scores_strided(
+        base, base + HI * DI * es, base + (HI * DI + DI) * es, L.dtype_code(dtype), B, T, HI,
+        DI, RS, RS, RS, got.data_ptr(), T, 1, L.stream_ptr(dev))
+    L.check(rc, "strided")
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-3), (torch.bfloat16, 2e-2)])
+def test_projection_front_end_fused(dev, dtype, tol):
+    """indexer_from_hidden (one GEMM read in place) against the float64 oracle
+    of project() + indexer (test_indexer.py:36-48 tolerance for fp32)."""
+    from lightning_indexer import indexer_from_hidden
+
+    B, T, D, H, d = 2, 160, 256, 8, 64
+    g = torch.Generator().manual_seed(5)
+    h = torch.randn(B, T, D, generator=g)
+    W_Q = torch.randn(D, H * d, generator=g) * 0.06
+    W_K = torch.randn(D, d, generator=g) * 0.06
+    W_W = torch.randn(D, H, generator=g) * 0.06
+    hd, Wq, Wk, Ww = (x.to(dtype) for x in (h, W_Q, W_K, W_W))
+    out = indexer_from_hidden(hd.to(dev), Wq.to(dev), Wk.to(dev), Ww.to(dev), H, d).cpu()
+    hq, hk, hw = (hd.double() @ W.double() for W in (Wq, Wk, Ww))
+    ref = O.indexer_scores(hq.view(B, T, H, d), hk, hw)
+    causal = torch.ones(T, T, dtype=torch.bool).tril()
+    err = float((out[:, causal].double() - ref[:, causal]).abs().max())
+    scale = float(ref[:, causal].abs().max())
+    assert err <= tol * max(1.0, scale), f"max abs err {err} (scale {scale})"
+    assert bool(torch.isneginf(out[:, ~causal]).all())
