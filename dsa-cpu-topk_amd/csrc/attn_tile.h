@@ -26,15 +26,33 @@ namespace dsa {
 
 constexpr int kListCap = 512;  // one 512-entry segment of the score row
 
+// This lane's slice of query row t, times scale_log2 (0 past the row).
+template <typename Tag, int EK>
+__device__ __forceinline__ void load_query(const typename Tag::raw* __restrict__ Q, int t,
+                                           int EQ, float scale_log2, float (&q)[EK]) {
+  const int lane = lane_id();
+  if (lane * EK < EQ) {
+    load_cvt<Tag, EK>(Q + static_cast<int64_t>(t) * EQ + lane * EK, q);
+#pragma unroll
+    for (int e = 0; e < EK; ++e) q[e] *= scale_log2;
+  } else {
+#pragma unroll
+    for (int e = 0; e < EK; ++e) q[e] = 0.f;
+  }
+}
+
 // Q/K/V point at this batch element: Q row t is Q + t*HQ*DQ, etc.
 // load4(s, sv) loads scores s..s+3 (s <= t, s % 4 == 0) of this query's row.
+// qpre: this lane's query slice from load_query, loaded early by the caller
+// (nullptr: loaded here).
 template <typename Tag, int EK, int EV, typename Load4>
 __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict__ Q,
                                              const typename Tag::raw* __restrict__ K,
                                              const typename Tag::raw* __restrict__ V, int t,
                                              int HQ, int DQ, int DV, float scale_log2,
                                              float thr, Load4&& load4, int* list,
-                                             float* __restrict__ out_row) {
+                                             float* __restrict__ out_row,
+                                             const float* qpre = nullptr) {
   using raw = typename Tag::raw;
   const int lane = lane_id();
   const int EQ = HQ * DQ;
@@ -47,13 +65,11 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
   const bool same_map = (DQ / EK) == (DV / EV);  // K and V slices cover the same head
 
   float q[EK];
-  if (kact) {
-    load_cvt<Tag, EK>(Q + static_cast<int64_t>(t) * EQ + lane * EK, q);
+  if (qpre != nullptr) {
 #pragma unroll
-    for (int e = 0; e < EK; ++e) q[e] *= scale_log2;
+    for (int e = 0; e < EK; ++e) q[e] = qpre[e];
   } else {
-#pragma unroll
-    for (int e = 0; e < EK; ++e) q[e] = 0.f;
+    load_query<Tag, EK>(Q, t, EQ, scale_log2, q);
   }
   float acc[EV];
 #pragma unroll

@@ -105,7 +105,15 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
   const raw* K = static_cast<const raw*>(a.K) + b * T * EQ;
   const raw* V = static_cast<const raw*>(a.V) + b * T * EVt;
 
-  // 2. rows 2w, 2w+1 of the block.
+  // 2. rows 2w, 2w+1 of the block.  Both query rows are loaded first, so
+  // their latency hides behind the first row's select.
+  float qpre[2][EK];
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int t = min(tile * 16 + 2 * wave + rr, T - 1);
+    load_query<Tag, EK>(Q, t, static_cast<int>(EQ), a.scale_log2, qpre[rr]);
+  }
+#pragma unroll
   for (int rr = 0; rr < 2; ++rr) {
     const int r = 2 * wave + rr;
     const int t = tile * 16 + r;
@@ -122,7 +130,7 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
           const float4 f = *reinterpret_cast<const float4*>(row + s);
           sv[0] = f.x; sv[1] = f.y; sv[2] = f.z; sv[3] = f.w;
         },
-        list, a.out + (b * T + t) * EVt);
+        list, a.out + (b * T + t) * EVt, qpre[rr]);
   }
 }
 
