@@ -122,6 +122,26 @@ __device__ __forceinline__ float group_bcast(float v) {
   }
 }
 
+// Max / sum of v over the lane pairs {l, l^32} and {l, l^16}, on the VALU
+// (v_permlane32_swap / v_permlane16_swap of v with itself: the two results
+// hold, for every lane l, v[l & ~M] and v[l | M], M = 32 or 16).
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Value of lane `src` (uniform) broadcast to the wave.
 template <typename T>
 __device__ __forceinline__ T wave_read_lane(T x, int src) {

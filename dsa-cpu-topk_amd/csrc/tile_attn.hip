@@ -300,8 +300,7 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[j][qt][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      mx = max_xor32(max_xor16(mx));  // over the 4 lane groups (VALU lane swaps)
       const float m_blk = mx * a.scale_log2;
       const bool up = m_blk > m[qt] + 8.f;
       const float m_new = up ? m_blk : m[qt];
@@ -383,8 +382,7 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     float lt = l[qt];
-    lt += __shfl_xor(lt, 16, kWave);
-    lt += __shfl_xor(lt, 32, kWave);
+    lt = sum_xor32(sum_xor16(lt));
     const float inv = 1.f / lt;  // lt == 0 only if nothing passed: NaN, as the reference
     if (tq[qt] < T) {
       float* orow = a.out + ((b * T + tq[qt]) * HQ + h) * static_cast<int64_t>(D);
