@@ -119,14 +119,20 @@ __device__ __forceinline__ void dma_tile(const uint16_t* __restrict__ src, int64
                                          int T, DSA_LDS uint8_t* dst, int wave, int lane) {
   using L = TileLds<D>;
   constexpr int PER_WAVE = L::BYTES / 1024 / (kNT / kWave);  // 1 KiB DMA instructions per wave
+  // 32-bit byte offsets against the uniform base (the host keeps a batch
+  // element's K and V under 4 GiB)
+  const char* base = reinterpret_cast<const char*>(src);
+  const uint32_t rowbytes = static_cast<uint32_t>(rowE) * 2u;
 #pragma unroll
   for (int i = 0; i < PER_WAVE; ++i) {
     const int ins = wave * PER_WAVE + i;
     const int P = ins * 64 + lane;  // physical chunk index this lane fills
     const int r = P / L::NCH, pc = P % L::NCH;
     const int lc = pc ^ (IS_K ? L::swz_k(r) : L::swz_v(r));
-    const int s = min(s0 + r, T - 1);
-    __builtin_amdgcn_global_load_lds(src + s * rowE + 8 * lc, dst + ins * 1024, 16, 0, 0);
+    const uint32_t s = static_cast<uint32_t>(min(s0 + r, T - 1));
+    const uint32_t off = s * rowbytes + 16u * static_cast<uint32_t>(lc);
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint16_t*>(base + off),
+                                     dst + ins * 1024, 16, 0, 0);
   }
 }
 
