@@ -89,6 +89,26 @@ __device__ __forceinline__ T wave_inclusive_sum(T x) {
   return static_cast<T>(v);
 }
 
+// Maximum and minimum of a float over the 64 lanes by the scan's DPP steps
+// (a lane with no source keeps its own value); the result is read from lane
+// 63.  NaN inputs are the caller's to exclude.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_keep_f32(float v) {
+  const int b = __float_as_int(v);
+  return __int_as_float(__builtin_amdgcn_update_dpp(b, b, CTRL, ROW_MASK, 0xf, false));
+}
+template <bool MAX>
+__device__ __forceinline__ float wave_extreme_f32(float v) {
+  auto op = [](float x, float y) { return MAX ? fmaxf(x, y) : fminf(x, y); };
+  v = op(v, dpp_keep_f32<0x111>(v));
+  v = op(v, dpp_keep_f32<0x112>(v));
+  v = op(v, dpp_keep_f32<0x114>(v));
+  v = op(v, dpp_keep_f32<0x118>(v));
+  v = op(v, dpp_keep_f32<0x142, 0xa>(v));
+  v = op(v, dpp_keep_f32<0x143, 0xc>(v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // DPP lane moves of a float inside 16-lane rows (VALU, no LDS round trip).
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
@@ -161,6 +181,10 @@ __device__ __forceinline__ T wave_sum(T v) {
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
   return v;
 }
+
+// Lanes whose predicate holds, as a 64-bit mask (the compare's own lane mask;
+// HIP's __ballot takes an int and re-materialises it).
+__device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
 
 __device__ __forceinline__ uint32_t popc64(uint64_t m) {
   return static_cast<uint32_t>(__popcll(m));

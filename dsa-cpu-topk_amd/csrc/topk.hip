@@ -32,6 +32,8 @@
 //
 // Rows longer than the largest register configuration use the streaming
 // kernel (same passes, the row re-read from global memory on every pass).
+#include <cmath>
+
 #include "dsa_device.h"
 #include "dsa_launch.h"
 
@@ -91,13 +93,14 @@ __device__ __forceinline__ bool in_prefix(uint32_t kk, uint32_t prefix) {
   else return (kk >> HI) == prefix;
 }
 
-// Finds the digit holding the krem-th largest key of an NB-bin histogram.
-// Thread tid owns bins [tid*BPT, tid*BPT+BPT).  Ends with a barrier after
-// which info[0] = digit, info[1] = rank of the wanted key inside the digit,
-// info[2] = keys in the digit.
-template <int NT, int NB>
-__device__ __forceinline__ void find_digit(const uint32_t* hist, uint32_t krem, uint32_t* wsum,
-                                           uint32_t* info) {
+// Finds the digits holding the r[q]-th largest keys of an NB-bin histogram
+// (one suffix scan for all R ranks).  Thread tid owns bins [tid*BPT,
+// tid*BPT+BPT).  Ends with a barrier after which, for each q, info[3q] =
+// digit, info[3q+1] = rank of the wanted key inside the digit, info[3q+2] =
+// keys in the digit.
+template <int NT, int NB, int R>
+__device__ __forceinline__ void find_digits(const uint32_t* hist, const uint32_t (&r)[R],
+                                            uint32_t* wsum, uint32_t* info) {
   constexpr int BPT = NB >= NT ? NB / NT : 1;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -121,21 +124,32 @@ __device__ __forceinline__ void find_digit(const uint32_t* hist, uint32_t krem, 
     tot += s;
   }
   const uint32_t above = tot - base - incl;  // keys in bins of higher threads
-  if (above < krem && above + local >= krem) {
-    uint32_t cum = above;
-    bool done = false;
 #pragma unroll
-    for (int i = BPT - 1; i >= 0; --i) {
-      if (!done && cum + h[i] >= krem) {
-        info[0] = static_cast<uint32_t>(lo + i);
-        info[1] = krem - cum;
-        info[2] = h[i];
-        done = true;
+  for (int q = 0; q < R; ++q) {
+    const uint32_t want = r[q];
+    if (above < want && above + local >= want) {
+      uint32_t cum = above;
+      bool done = false;
+#pragma unroll
+      for (int i = BPT - 1; i >= 0; --i) {
+        if (!done && cum + h[i] >= want) {
+          info[3 * q] = static_cast<uint32_t>(lo + i);
+          info[3 * q + 1] = want - cum;
+          info[3 * q + 2] = h[i];
+          done = true;
+        }
+        cum += h[i];
       }
-      cum += h[i];
     }
   }
   block_sync_lds();
+}
+
+template <int NT, int NB>
+__device__ __forceinline__ void find_digit(const uint32_t* hist, uint32_t krem, uint32_t* wsum,
+                                           uint32_t* info) {
+  const uint32_t r[1] = {krem};
+  find_digits<NT, NB, 1>(hist, r, wsum, info);
 }
 
 // One radix pass over the keys `visit` enumerates (keys equal to kKeyNone
@@ -216,14 +230,16 @@ __device__ __forceinline__ void emit_indices(int32_t* out, int64_t nchunks, uint
   }
 }
 
-// k-th largest of n candidate keys in LDS that all share their bits above
-// bit `low` (those bits are `prefix`), by one wave: MSD passes over at most 8
-// of the remaining bits, each a 256-bin histogram in `hist` (wave-private
-// LDS) built with ds_add and a wave suffix scan -- wave-level syncs only, no
-// block barrier.  A digit holding a single key ends the search early.
-__device__ __forceinline__ uint32_t wave_select_cand(const uint32_t* cand, uint32_t n,
-                                                     uint32_t prefix, int low, uint32_t krem,
-                                                     uint32_t* hist) {
+// krem-th largest of candidate keys that all share their bits above bit
+// `low` (those bits are `prefix`), by one wave.  visit(f) calls f(key) for
+// this lane's share of the candidates (in LDS), so every pass re-reads them.
+// MSD passes over at most 8 of the remaining bits, each a 256-bin histogram
+// in `hist` (wave-private LDS) built with ds_add and a wave suffix scan --
+// wave-level syncs only, no block barrier.  A digit holding a single key
+// ends the search early.
+template <typename Visit>
+__device__ __forceinline__ uint32_t wave_select_keys(Visit&& visit, uint32_t prefix, int low,
+                                                     uint32_t krem, uint32_t* hist) {
   const int lane = threadIdx.x & (kWave - 1);
   int shift = low;
   while (shift > 0) {
@@ -233,10 +249,9 @@ __device__ __forceinline__ uint32_t wave_select_cand(const uint32_t* cand, uint3
     const int hi = shift + bits;  // may be 32: 64-bit shifts below
     reinterpret_cast<uint4*>(hist)[lane] = make_uint4(0u, 0u, 0u, 0u);
     wave_lds_sync();
-    for (uint32_t i = lane; i < n; i += kWave) {
-      const uint32_t kk = cand[i];
+    visit([&](uint32_t kk) {
       if ((static_cast<uint64_t>(kk) >> hi) == prefix) atomicAdd(&hist[(kk >> shift) & mask], 1u);
-    }
+    });
     wave_lds_sync();
     const uint4 h4 = reinterpret_cast<const uint4*>(hist)[lane];
     const uint32_t h[4] = {h4.x, h4.y, h4.z, h4.w};
@@ -265,15 +280,26 @@ __device__ __forceinline__ uint32_t wave_select_cand(const uint32_t* cand, uint3
     wave_lds_sync();  // histogram reads done before the next pass clears it
     if (shift > 0 && cnt == 1u) {
       uint32_t hit = 0;
-      for (uint32_t i = lane; i < n; i += kWave) {
-        const uint32_t kk = cand[i];
+      visit([&](uint32_t kk) {
         if ((kk >> shift) == prefix) hit = kk;
-      }
+      });
       const uint64_t m = __ballot(hit != 0u);
       return wave_read_lane(hit, __ffsll(static_cast<unsigned long long>(m)) - 1);
     }
   }
   return prefix;
+}
+
+// wave_select_keys over n candidates stored contiguously at cand.
+__device__ __forceinline__ uint32_t wave_select_cand(const uint32_t* cand, uint32_t n,
+                                                     uint32_t prefix, int low, uint32_t krem,
+                                                     uint32_t* hist) {
+  const uint32_t lane = threadIdx.x & (kWave - 1);
+  return wave_select_keys(
+      [&](auto&& f) {
+        for (uint32_t i = lane; i < n; i += kWave) f(cand[i]);
+      },
+      prefix, low, krem, hist);
 }
 
 template <bool VEC>
@@ -467,6 +493,32 @@ __global__ __launch_bounds__(NT, (V <= 32 && NT <= 512) ? 8 : 4) void topk_reg_k
 // ---------------------------------------------------------------------------
 // Streaming kernel: any row length; the row is re-read on every pass.
 // ---------------------------------------------------------------------------
+// Exact k-th largest key of the nvalid entries at src by three radix passes
+// that each re-read the row; krem is left at the rank of the wanted key among
+// the keys equal to it.  hist: kBins words of LDS.
+template <int NT, bool VEC>
+__device__ __forceinline__ uint32_t stream_select(const float* __restrict__ src, int64_t nvalid,
+                                                  int k, uint32_t* hist, uint32_t* wsum,
+                                                  uint32_t* info, uint32_t& krem) {
+  const int tid = threadIdx.x;
+  const int64_t nchunks = (nvalid + 4 * NT - 1) / (4 * NT);
+  auto visit = [&](auto&& f) {
+    for (int64_t j = 0; j < nchunks; ++j) {
+      uint32_t kk[4];
+      load_keys4<VEC>(src, (j * NT + tid) * 4, nvalid, kk);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) f(kk[c]);
+    }
+  };
+  uint32_t prefix = 0, cnt = 0, thr_key = 0;
+  krem = static_cast<uint32_t>(k);
+  bool found = radix_pass<NT, kS1, kP1>(visit, hist, wsum, info, prefix, krem, cnt, true, thr_key);
+  if (!found) found = radix_pass<NT, kS2, kB2>(visit, hist, wsum, info, prefix, krem, cnt, true,
+                                             thr_key);
+  if (!found) radix_pass<NT, 0, kB3>(visit, hist, wsum, info, prefix, krem, cnt, false, thr_key);
+  return found ? thr_key : prefix;
+}
+
 template <int NT, bool VEC>
 __global__ __launch_bounds__(NT) void topk_stream_kernel(SelectArgs a) {
   __shared__ uint32_t hist[kBins];
@@ -482,27 +534,367 @@ __global__ __launch_bounds__(NT) void topk_stream_kernel(SelectArgs a) {
     return;
   }
   const float* __restrict__ src = a.scores + row * a.ld;
-  const int64_t nchunks = (nvalid + 4 * NT - 1) / (4 * NT);
-  auto chunk = [&](int64_t j, uint32_t(&kk)[4]) {
-    load_keys4<VEC>(src, (j * NT + tid) * 4, nvalid, kk);
+  uint32_t krem;
+  const uint32_t thr_key = stream_select<NT, VEC>(src, nvalid, k, hist, wsum, info, krem);
+  if (tid == 0) a.thr[row] = key_to_float(thr_key);
+  if (a.idx != nullptr) {
+    const int64_t nchunks = (nvalid + 4 * NT - 1) / (4 * NT);
+    emit_indices<NT>(a.idx + row * static_cast<int64_t>(k), nchunks, thr_key, krem, wsum,
+                     [&](int64_t j, uint32_t(&kk)[4]) {
+                       load_keys4<VEC>(src, (j * NT + tid) * 4, nvalid, kk);
+                     });
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Bracket kernel: thresholds of long rows in one pass over the row.
+// ---------------------------------------------------------------------------
+constexpr int kBrBins = 1024;    // sample histogram: value bins over the sample's range
+constexpr int kFinBins = 256;    // finishing wave's value bins over the kept values
+constexpr int kFinGather = 64;   // kept values of one finishing bin ranked in registers
+
+// Bin of v among top + 1 bins linear in value: (v - lo) * scale clamped to
+// [0, top].  For finite lo and scale >= 0 it is monotone non-decreasing in v
+// (each rounding step is monotone, then a clamp and a truncation), and -0
+// and +0 share a bin.
+__device__ __forceinline__ int value_bin(float v, float lo, float scale, float top) {
+  return static_cast<int>(__builtin_amdgcn_fmed3f((v - lo) * scale, 0.0f, top));
+}
+
+// A sample of four 4*NT-entry chunks spread evenly over the row is held in
+// registers and ranked approximately: one LDS histogram over kBrBins bins
+// linear in VALUE between the sample's minimum and maximum (bins follow the
+// data's density, so ds_add rarely collides).  With m of the row's n entries
+// in the sample, the row's k-th largest sits near sample rank e = k*m/n; the
+// bins holding sample ranks e - delta and e + delta (delta = five standard
+// deviations of that rank, plus 2), widened by a bin each side, give a value
+// interval [lo, hi).  The rest of the row then streams through once,
+// compared as floats: each thread counts its values below hi (NaN is not)
+// and keeps those in [lo, hi) in its own LDS column -- every value is
+// written to the column's next free slot and the slot index advances only
+// when the value is kept, so there is no branch and no atomic per value.
+// These sets are intervals of the key order (NaN largest, -0 == +0), so the
+// interval only steers the search and exactness comes from the check: with
+// above = n - (values below hi), when above < k <= above + kept the row's
+// k-th largest is the (k - above)-th largest kept value; otherwise (the
+// sample missed, or a column or the kept list outgrew LDS) the row is
+// selected exactly by the streaming radix passes.  The kept values are then
+// compacted into one list and one wave finishes: a histogram of them over
+// kFinBins value bins between their minimum and maximum, then the few values
+// of the bin holding the wanted rank are ranked against each other in
+// registers (a bin holding more than kFinGather, i.e. heavy ties, takes
+// radix passes over the kept keys).  A row of at most four chunks is its own
+// sample (delta = 0).
+template <int NT>
+__global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
+  constexpr int NW = NT / kWave;
+  constexpr int CH = 4 * NT;  // entries per chunk (one float4 per thread)
+  constexpr int CAP = 19;     // LDS column slots per thread
+  static_assert(NT == 256 && kBrBins == 4 * NT, "layout below assumes 4 waves of 4 bins");
+  static_assert(CAP * NT >= kCandCap + kFinBins + kFinGather, "finish fits the columns");
+  // lds: sample histogram [0, kBrBins), then per-thread columns (slot s of
+  // thread t at s*NT + t), then the compacted kept list [0, n_kept) with the
+  // finishing wave's histogram and gather list at kCandCap.
+  __shared__ __align__(16) uint32_t lds[CAP * NT];
+  __shared__ uint32_t wsum[NW];
+  __shared__ uint32_t info[6];
+  __shared__ float wext[2 * NW];
+  __shared__ uint32_t wcnt[NW], wbad[NW];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wid = tid / kWave;
+  int64_t row, nvalid;
+  row_of_block(a, row, nvalid);
+  const int k = a.k;
+  if (nvalid < k) {
+    emit_short_row<NT>(a, row);
+    return;
+  }
+  const float* __restrict__ src = a.scores + row * a.ld;
+  const char* row_bytes = reinterpret_cast<const char*>(src);
+  const int nv = static_cast<int>(nvalid);  // the host keeps rows below 2^20 entries
+  const int last4 = (nv - 1) & ~3;
+  const int nc = (nv + CH - 1) / CH;
+  const bool whole = nc <= 4;
+  // Clamped float4 load of chunk j: no load behind a branch.
+  auto load4 = [&](int j) -> float4 {
+    const uint32_t off = static_cast<uint32_t>(min((j * NT + tid) * 4, last4)) * 4u;
+    return *reinterpret_cast<const float4*>(row_bytes + off);
   };
-  auto visit = [&](auto&& f) {
-    for (int64_t j = 0; j < nchunks; ++j) {
-      uint32_t kk[4];
-      chunk(j, kk);
+  auto sample_chunk = [&](int s) { return whole ? s : (s * nc) / 4; };
+  // Sample entry i of this thread lies inside the row (always, unless whole).
+  auto sample_in = [&](int i) { return (sample_chunk(i / 4) * NT + tid) * 4 + (i & 3) < nv; };
+
+  float sv[16];
+  {
+    float4 f[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) f(kk[c]);
+    for (int s = 0; s < 4; ++s) f[s] = load4(sample_chunk(s));
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      sv[4 * s] = f[s].x;
+      sv[4 * s + 1] = f[s].y;
+      sv[4 * s + 2] = f[s].z;
+      sv[4 * s + 3] = f[s].w;
+    }
+  }
+  uint32_t r1 = static_cast<uint32_t>(k), r2 = static_cast<uint32_t>(k);
+  if (!whole) {
+    const float frac = static_cast<float>(4 * CH) / static_cast<float>(nv);
+    const float e = static_cast<float>(k) * frac;
+    const float delta = 5.0f * sqrtf(e * (1.0f - frac)) + 2.0f;
+    r1 = static_cast<uint32_t>(max(1.0f, floorf(e - delta)));
+    r2 = static_cast<uint32_t>(min(static_cast<float>(4 * CH), ceilf(e + delta)));
+  }
+
+  // Range of the sample (NaN ignored by fmax/fmin; entries past the row
+  // become NaN here).  An infinite end is replaced by the finite range.
+  auto block_range = [&](bool finite_only, float& vmin, float& vmax) {
+    float hi = -__builtin_huge_valf(), lo = __builtin_huge_valf();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float v = (!whole || sample_in(i)) ? sv[i] : __builtin_nanf("");
+      if (finite_only) v = fabsf(v) <= __FLT_MAX__ ? v : __builtin_nanf("");
+      hi = fmaxf(hi, v);
+      lo = fminf(lo, v);
+    }
+    hi = wave_extreme_f32<true>(hi);
+    lo = wave_extreme_f32<false>(lo);
+    if (lane == 0) {
+      wext[wid] = hi;
+      wext[NW + wid] = lo;
+    }
+    block_sync_lds();
+    vmax = -__builtin_huge_valf();
+    vmin = __builtin_huge_valf();
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      vmax = fmaxf(vmax, wext[w]);
+      vmin = fminf(vmin, wext[NW + w]);
     }
   };
-  uint32_t prefix = 0, krem = static_cast<uint32_t>(k), cnt = 0, thr_key = 0;
-  bool found = radix_pass<NT, kS1, kP1>(visit, hist, wsum, info, prefix, krem, cnt, true, thr_key);
-  if (!found) found = radix_pass<NT, kS2, kB2>(visit, hist, wsum, info, prefix, krem, cnt, true,
-                                             thr_key);
-  if (!found) radix_pass<NT, 0, kB3>(visit, hist, wsum, info, prefix, krem, cnt, false, thr_key);
-  if (!found) thr_key = prefix;
-  if (tid == 0) a.thr[row] = key_to_float(thr_key);
-  if (a.idx != nullptr)
-    emit_indices<NT>(a.idx + row * static_cast<int64_t>(k), nchunks, thr_key, krem, wsum, chunk);
+#pragma unroll
+  for (int q = 0; q < kBrBins / (4 * NT); ++q)
+    reinterpret_cast<uint4*>(lds)[q * NT + tid] = make_uint4(0u, 0u, 0u, 0u);
+  float vmin, vmax;
+  block_range(false, vmin, vmax);
+  if (!(vmax < __builtin_huge_valf()) || !(vmin > -__builtin_huge_valf())) {
+    block_sync_lds();  // every wave has read wext
+    block_range(true, vmin, vmax);
+  }
+  // No finite value, a single one, or a range that overflows: one bin.
+  const float range = vmax - vmin;
+  float scale = static_cast<float>(kBrBins) / range;
+  if (!(range > 0.0f) || !(scale <= __FLT_MAX__)) {
+    scale = 0.0f;
+    vmin = 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if (!whole || sample_in(i))
+      atomicAdd(&lds[value_bin(sv[i], vmin, scale, kBrBins - 1)], 1u);
+  }
+  block_sync_lds();
+  {
+    const uint32_t r[2] = {r1, r2};
+    find_digits<NT, kBrBins, 2>(lds, r, wsum, info);
+  }
+  // Value interval [flo, fhi) covering bins b2 .. b1 (b1 >= b2) and one bin
+  // either side (bin edges below are recomputed, not the binning's own
+  // rounding); the end bins reach out to -inf and +inf.
+  const int b1 = min(static_cast<int>(info[0]) + 1, kBrBins - 1);
+  const int b2 = max(static_cast<int>(info[3]) - 1, 0);
+  const float flo = b2 == 0 ? -__builtin_huge_valf() : vmin + static_cast<float>(b2) / scale;
+  const float fhi = b1 == kBrBins - 1 ? __builtin_huge_valf()
+                                      : vmin + static_cast<float>(b1 + 1) / scale;
+
+  // Classify.  find_digits' closing barrier ordered every histogram read.
+  uint32_t below = 0, kc = 0;  // this thread: valid values below fhi; kept
+  bool bad = false;            // wave-uniform: a column came near CAP
+  uint32_t* col = lds + tid;
+  auto take = [&](float v, bool valid) {
+    const bool lt = valid && v < fhi;
+    const bool kp = lt && !(v < flo);
+    col[kc * NT] = __float_as_uint(v);  // the next free slot; kept only if kc advances
+    below += lt ? 1u : 0u;
+    kc += kp ? 1u : 0u;
+  };
+  // Before every 4 values: a column with fewer than 4 free slots stops the
+  // wave (the row then takes the exact passes).
+  auto room = [&]() {
+    bad = bad || ballot(kc > static_cast<uint32_t>(CAP - 4)) != 0u;
+    return !bad;
+  };
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    if (room()) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) take(sv[4 * s + c], !whole || sample_in(4 * s + c));
+    }
+  }
+
+  if (!whole && !bad) {
+    // Chunks outside the sample, 4 per step, the next step's loads in flight
+    // while this step's values are classified.
+    const int ns = nc - 4;
+    auto chunk_of = [&](int u) {  // u-th chunk that is not a sample chunk
+      int j = u;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) j += ((s * nc) / 4 <= j) ? 1 : 0;
+      return j;
+    };
+    const int nsteps = (ns + 3) / 4;
+    float4 cur[4];
+    int jc[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      jc[q] = chunk_of(min(q, ns - 1));
+      cur[q] = load4(jc[q]);
+    }
+    for (int it = 0; it < nsteps; ++it) {
+      float4 nxt[4];
+      int jn[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        jn[q] = chunk_of(min(4 * (it + 1) + q, ns - 1));
+        nxt[q] = load4(jn[q]);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float fv[4] = {cur[q].x, cur[q].y, cur[q].z, cur[q].w};
+        if (4 * it + q < ns && room()) {  // else a repeated load past the last chunk
+          if ((jc[q] + 1) * CH <= nv) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) take(fv[c], true);
+          } else {
+            const int p0 = (jc[q] * NT + tid) * 4;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) take(fv[c], p0 + c < nv);
+          }
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        cur[q] = nxt[q];
+        jc[q] = jn[q];
+      }
+    }
+  }
+
+  // Block totals: values below fhi and kept, and whether a column filled.
+  {
+    const uint32_t wb = wave_read_lane(wave_inclusive_sum((below << 12) | kc), kWave - 1);
+    if (lane == 0) {
+      wcnt[wid] = wb;
+      wbad[wid] = bad ? 1u : 0u;
+    }
+  }
+  // Kept values to registers before the columns are overwritten by the list.
+  uint32_t mine[CAP];
+#pragma unroll
+  for (int s = 0; s < CAP; ++s) mine[s] = col[s * NT];
+  uint32_t ktot;
+  const uint32_t kbase = block_exclusive_sum<NT>(kc, wsum, ktot);  // its barriers order the reads
+  uint32_t tot_below = 0;
+  bool any_bad = false;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    tot_below += wcnt[w] >> 12;
+    any_bad = any_bad || wbad[w] != 0u;
+  }
+  const uint32_t ku = static_cast<uint32_t>(k);
+  const uint32_t tot_above = static_cast<uint32_t>(nv) - tot_below;
+  if (!any_bad && ktot <= static_cast<uint32_t>(kCandCap) && tot_above < ku &&
+      ku <= tot_above + ktot) {
+#pragma unroll
+    for (int s = 0; s < CAP; ++s)
+      if (static_cast<uint32_t>(s) < kc) lds[kbase + s] = mine[s];
+    block_sync_lds();
+    if (wid != 0) return;
+    const uint32_t krem = ku - tot_above;
+    auto visit_kept = [&](auto&& f) {
+      for (uint32_t i = lane; i < ktot; i += kWave) f(__uint_as_float(lds[i]));
+    };
+    // Value bins over the kept values' own range (all below fhi, so NaN is
+    // never kept; -inf may be).
+    float khi = -__builtin_huge_valf(), klo = __builtin_huge_valf();
+    visit_kept([&](float v) {
+      khi = fmaxf(khi, v);
+      klo = fminf(klo, v);
+    });
+    khi = wave_extreme_f32<true>(khi);
+    klo = wave_extreme_f32<false>(klo);
+    const float krange = khi - klo;
+    const float ks = static_cast<float>(kFinBins) / krange;
+    // Bins need a finite range (klo > -inf); else all equal or -inf kept.
+    const bool binned = krange > 0.0f && krange <= __FLT_MAX__ && ks <= __FLT_MAX__;
+    uint32_t* fh = lds + kCandCap;
+    reinterpret_cast<uint4*>(fh)[lane] = make_uint4(0u, 0u, 0u, 0u);
+    wave_lds_sync();
+    if (binned) visit_kept([&](float v) { atomicAdd(&fh[value_bin(v, klo, ks, kFinBins - 1)], 1u); });
+    else if (lane == 0) fh[0] = ktot;  // one bin: the radix passes below
+    wave_lds_sync();
+    // Suffix scan over the bins (4 per lane) for the bin holding rank krem.
+    const uint4 h4 = reinterpret_cast<const uint4*>(fh)[lane];
+    const uint32_t h[4] = {h4.x, h4.y, h4.z, h4.w};
+    const uint32_t local = h[0] + h[1] + h[2] + h[3];
+    const uint32_t incl = wave_inclusive_sum(local);
+    const uint32_t abv = wave_read_lane(incl, kWave - 1) - incl;
+    const bool here = abv < krem && abv + local >= krem;
+    uint32_t bsel = 0, brank = 0, bcnt = 0;
+    if (here) {
+      uint32_t cum = abv;
+#pragma unroll
+      for (int i = 3; i >= 0; --i) {
+        if (bcnt == 0u && cum + h[i] >= krem) {
+          bsel = 4u * lane + i;
+          brank = krem - cum;
+          bcnt = h[i];
+        }
+        cum += h[i];
+      }
+    }
+    const int srcl = __ffsll(static_cast<unsigned long long>(ballot(here))) - 1;
+    bsel = wave_read_lane(bsel, srcl);
+    brank = wave_read_lane(brank, srcl);
+    bcnt = wave_read_lane(bcnt, srcl);
+    float res;
+    if (binned && bcnt <= static_cast<uint32_t>(kFinGather)) {
+      // Gather the chosen bin's values, then rank them against each other:
+      // the wanted one has fewer than brank greater and at least brank
+      // greater-or-equal.
+      uint32_t* gl = fh + kFinBins;
+      uint32_t ng = 0;
+      visit_kept([&](float v) {
+        const bool in = value_bin(v, klo, ks, kFinBins - 1) == static_cast<int>(bsel);
+        const uint64_t m = ballot(in);
+        if (in) gl[ng + lanes_below(m)] = __float_as_uint(v);
+        ng += popc64(m);
+      });
+      wave_lds_sync();
+      const float mv = lane < static_cast<int>(bcnt) ? __uint_as_float(gl[lane]) : 0.0f;
+      uint32_t gt = 0, ge = 0;
+      for (uint32_t j = 0; j < bcnt; ++j) {
+        const float o = __uint_as_float(gl[j]);
+        gt += (o > mv) ? 1u : 0u;
+        ge += (o >= mv) ? 1u : 0u;
+      }
+      const bool hit = lane < static_cast<int>(bcnt) && gt < brank && ge >= brank;
+      res = __int_as_float(wave_read_lane(
+          __float_as_int(mv), __ffsll(static_cast<unsigned long long>(ballot(hit))) - 1));
+    } else {
+      // Heavy ties or no finite range: exact radix passes over the kept keys.
+      const uint32_t tk = wave_select_keys(
+          [&](auto&& f) { visit_kept([&](float v) { f(float_to_key(v)); }); }, 0u, 32, krem, fh);
+      res = key_to_float(tk);
+    }
+    if (lane == 0) a.thr[row] = res + 0.0f;  // -0 reported as +0, as the key order does
+    return;
+  }
+  uint32_t krem;
+  const uint32_t tk = stream_select<NT, true>(src, nvalid, k, lds, wsum, info, krem);
+  if (tid == 0) a.thr[row] = key_to_float(tk);
 }
 
 template <int NT, int V, int P1>
@@ -512,6 +904,23 @@ hipError_t launch_reg(const SelectArgs& a, bool vec, hipStream_t stream) {
     hipLaunchKernelGGL((topk_reg_kernel<NT, V, P1, true>), grid, dim3(NT), 0, stream, a);
   else
     hipLaunchKernelGGL((topk_reg_kernel<NT, V, P1, false>), grid, dim3(NT), 0, stream, a);
+  return hipGetLastError();
+}
+
+// The bracket kernel pays off when the keys it keeps fit LDS with room to
+// spare: expected kept keys at the longest row, (2*delta + 1) sample ranks
+// scaled by n/m, at most half of kCandCap.
+bool bracket_fits(int64_t cap, int k) {
+  if (cap <= 4096 || cap > (int64_t{1} << 20)) return false;
+  const double frac = 4096.0 / static_cast<double>(cap);
+  const double e = static_cast<double>(k) * frac;
+  const double delta = 5.0 * std::sqrt(e * (1.0 - frac)) + 2.0;
+  return (2.0 * delta + 1.0) / frac <= 0.5 * kCandCap;
+}
+
+hipError_t launch_bracket(const SelectArgs& a, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(a.rows));
+  hipLaunchKernelGGL((topk_bracket_kernel<256>), grid, dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -538,6 +947,8 @@ hipError_t launch_topk(const float* scores, int64_t rows, int64_t n, int64_t ld,
   // Rows above 8K entries use a 12-bit first digit: hot digits of real
   // score rows spread over twice the bins (fewer same-address LDS atomics)
   // and the chosen digit leaves half the candidates.
+  // Threshold-only rows above 4K entries: one pass over HBM (bracket kernel).
+  if (idx == nullptr && vec && bracket_fits(cap, k)) return launch_bracket(a, stream);
   if (cap <= 512) return launch_reg<128, 4, 11>(a, vec, stream);
   if (cap <= 1024) return launch_reg<128, 8, 11>(a, vec, stream);
   if (cap <= 2048) return launch_reg<256, 8, 11>(a, vec, stream);

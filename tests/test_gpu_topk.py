@@ -37,6 +37,7 @@ def check_rows(x_cpu, k, dev, causal=False, what=""):
     (8, 1, 1), (16, 5, 3), (33, 100, 7), (7, 256, 1), (5, 256, 256), (9, 513, 32),
     (4, 1000, 999), (64, 2048, 128), (8, 4096, 256), (4, 8191, 100), (3, 16384, 2048),
     (2, 32768, 5000), (2, 40000, 1234), (1, 100003, 77),
+    (3, 6000, 700), (2, 20000, 64), (2, 24576, 1000),
 ])
 def test_random_rows(dev, rows, n, k):
     check_rows(cpu_randn((rows, n), rows * 1000 + n), k, dev, what="randn")
@@ -62,6 +63,32 @@ def test_special_values(dev):
     x[3, :] = -0.0
     for k in (1, 2, 150, 300):
         check_rows(x, k, dev, what="special")
+
+
+def test_bracket_path_misses_fall_back(dev):
+    """Threshold-only rows above 4096 entries are selected in one pass from a
+    bracket that an evenly spread 4096-entry sample (chunks 0, 4, 8, 12 of
+    1024 entries here) predicts.  Rows that the sample misrepresents, or whose
+    bracket holds more keys than fit on chip, take the exact fallback: every
+    row must still be bit-exact."""
+    n = 16384
+    x = cpu_randn((12, n), 77)
+    x[1, 1024:2048] += 100.0                      # large values in a chunk the sample skips
+    x[2, 1024:4096] -= 100.0                      # small values the sample skips
+    x[3] = 1.0                                    # one value: every key kept
+    x[4] = torch.randint(0, 3, (n,), generator=torch.Generator().manual_seed(4)).float()
+    x[5] = torch.sort(x[5]).values                # ascending row
+    x[6, 4096:5120] = float("inf")                # a sample chunk of +inf
+    x[7, ::97] = float("nan")                     # NaN, the largest in torch.topk's order
+    x[8, : n // 2] = float("-inf")                # half -inf
+    x[9, 100:] = float("-inf")                    # almost all -inf
+    x[10] = x[10] * 1e30                          # wide range
+    x[11, 777] = 3e38                             # one huge outlier
+    xg = x.to(dev)
+    for k in (1, 100, 1024, 2048, 3000, 8000, 16383, 16384):
+        say(f"topk bracket misses k={k}")
+        torch.testing.assert_close(topk_threshold(xg, k).cpu(), O.topk_threshold(x, k),
+                                   rtol=0, atol=0, equal_nan=True, msg=f"k={k}")
 
 
 def test_reference_extension_test_cases(dev):
@@ -133,6 +160,8 @@ def test_causal_c4_shape_properties(dev):
     s = torch.randn((1, T, T), generator=g, device=dev, dtype=torch.float32)
     s = torch.where(torch.rand((1, T, T), generator=g, device=dev) < 0.05, 0.0, s)  # zero ties
     thr, idx = topk_indices(s, k, causal=True)
+    # the threshold-only entry point (one-pass bracket kernel) agrees
+    assert torch.equal(topk_threshold(s, k, causal=True), thr)
     torch.cuda.synchronize()
     tril = torch.ones(T, T, dtype=torch.bool, device=dev).tril()
     masked = s.masked_fill(~tril, float("-inf"))
