@@ -16,7 +16,13 @@ one kernel).  Prints ONE JSON line:
                rows of real config-4 indexer scores): algorithmic bytes
                4*sum(t+1) (+ outputs) / duration, against 8 TB/s
   split        the split forward (indexer, select, attention) at config 1
+  sweep_c2     fused and split forwards over config 2's (B, k) sweep at T=512,
+               beside the reference's published fused Triton times there
   split_c3/c4  the split forward at configs 3 (fp32) and 4 (bf16), per stage
+  projection   the indexer's projection front end (one GEMM + strided entry
+               vs three GEMMs)
+  stream       batches of configs 2-4 one after another, two-stream
+               pipelined, and captured in one HIP graph
   cpu_baseline the reference's CPU path restated (oracle/, torch-vectorised
                fp32 forward) on the host cores, plus the AVX-512 k-th-largest
                (the reference's own topk_avx512.cpp from oracle/_ref when it
@@ -158,6 +164,36 @@ def bench_split(dev, reps=50):
     for _ in range(5):
         fwd()
     return time_events(fwd, reps, torch.cuda.current_stream(dev))
+
+
+# Config 2 sweep at T=512 with the reference's published fused Triton times
+# on its own GPU (README.md:50-54; RTX PRO 6000 Blackwell).
+C2_SWEEP = ((4, 64, 1.34), (16, 64, 5.66), (16, 128, 5.67), (32, 64, 11.98), (64, 64, 25.96))
+
+
+def bench_sweep_c2(dev, reps=50):
+    """Fused and split forwards over the config-2 (B, k) sweep."""
+    import torch
+
+    import dsa_attention as D
+
+    stream = torch.cuda.current_stream(dev)
+    res = []
+    for B, k, ref_ms in C2_SWEEP:
+        cfg = dict(C1, B=B, k=k)
+        ins = gpu_inputs(cfg, torch.float32, dev, seed=B + k)
+        fused = lambda: D.dsa_fused_hip(*ins, k)  # noqa: E731
+        split = lambda: D.dsa_split_hip(*ins, k)  # noqa: E731
+        warm(fused, 0.1)
+        tf = time_events(fused, reps, stream)
+        warm(split, 0.1)
+        ts = time_events(split, reps, stream)
+        res.append({"B": B, "T": cfg["T"], "k": k,
+                    "fused_ms": round(tf * 1e3, 4), "split_ms": round(ts * 1e3, 4),
+                    "fused_query_tokens_per_s": round(B * cfg["T"] / tf, 1),
+                    "reference_fused_ms": ref_ms, "speedup_vs_reference": round(ref_ms / (tf * 1e3), 1)})
+        del ins
+    return res
 
 
 C3 = dict(B=4, T=4096, k=256, HI=8, DI=64, HQ=8, DQ=64, DV=64)
@@ -519,6 +555,8 @@ def main():
         "split": {"ms_per_step": round(split_s * 1e3, 5),
                   "value": round(B * T / split_s, 1), "unit": "query tokens/s"},
     }
+    log("bench: config 2 sweep")
+    out["sweep_c2"] = bench_sweep_c2(dev)
     if not args.no_select:
         log("bench: select at config 4")
         out["topk_select"] = bench_select_c4(dev)

@@ -182,6 +182,14 @@ __device__ __forceinline__ T wave_sum(T v) {
   return v;
 }
 
+// Bin of v among top + 1 bins linear in value: (v - lo) * scale clamped to
+// [0, top].  For finite lo and scale >= 0 it is monotone non-decreasing in v
+// (each rounding step is monotone, then a clamp and a truncation), and -0
+// and +0 share a bin.
+__device__ __forceinline__ int value_bin(float v, float lo, float scale, float top) {
+  return static_cast<int>(__builtin_amdgcn_fmed3f((v - lo) * scale, 0.0f, top));
+}
+
 // Lanes whose predicate holds, as a 64-bit mask (the compare's own lane mask;
 // HIP's __ballot takes an int and re-materialises it).
 __device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }

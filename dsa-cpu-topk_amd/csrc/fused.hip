@@ -6,13 +6,14 @@
 //      t0+4(w%4) .. +3 over one half (w/4) of their causal key range, into
 //      LDS rows shared by the block;
 //   -- one block barrier --
-//   2. wave w takes rows 2w and 2w+1: radix-select of the k_eff-th largest
-//      (wave_select.h), then sparse attention over keys with score >= thr
+//   2. wave w takes rows 2w and 2w+1: the k_eff-th largest by a value-bin
+//      histogram (wave_select.h), then sparse attention over keys with score >= thr
 //      (attn_tile.h).
 // The score rows never touch HBM.  Splitting the indexer's key range over
 // wave pairs and giving each wave two rows (not four) doubles the waves that
 // hide the gathers' memory latency, at the same MFMA work.  Blocks run
-// longest queries first, spread evenly over the XCDs (causal_block_tile).
+// longest queries first, spread evenly over the XCDs, or, when the grid is
+// resident two blocks per CU, one long and one short tile per CU (block_tile).
 //
 // LDS per block: 16 score rows of RS floats, RS = round_up(T,32) + 16 (the
 // +16 puts consecutive rows on different banks for the MFMA epilogue
@@ -39,9 +40,31 @@ struct FusedArgs {
   float scale_log2;
   float* out;
   int RS;
+  int pair_cus;  // > 0: pair long and short tiles on each CU (see block_tile)
 };
 
 int row_stride(int T) { return ((T + 31) / 32) * 32 + 16; }
+
+// Block -> (batch element, 16-query tile).  By default longest tiles first
+// (causal_block_tile).  When the whole grid is resident with two blocks per
+// CU (pair_cus = the CU count, a multiple of B), block i and block
+// i + pair_cus share a CU (workgroups go round-robin over the XCDs and then
+// over each XCD's CUs): the first pair_cus blocks take the longest tiles in
+// descending order and the rest the shortest in ascending order, so every CU
+// holds one long and one short tile and the CUs' work evens out.  The batch
+// element stays bid % B in both halves, so each XCD keeps its batch
+// elements' K/V rows in its L2.
+__device__ __forceinline__ void block_tile(uint32_t bid, int64_t B, int tiles, int pair_cus,
+                                           int64_t& b, int& tile) {
+  if (pair_cus > 0) {
+    const uint32_t cus = static_cast<uint32_t>(pair_cus);
+    const uint32_t j = bid < cus ? bid : bid - cus;
+    b = static_cast<int64_t>(j) % B;
+    tile = bid < cus ? tiles - 1 - static_cast<int>(j / B) : static_cast<int>(j / B);
+  } else {
+    causal_block_tile(bid, B, tiles, b, tile);
+  }
+}
 constexpr int kFusedWaves = 8;
 size_t fused_lds_bytes(int T) {
   return static_cast<size_t>(16) * row_stride(T) * 4 + kFusedWaves * 256 * 4 +
@@ -62,7 +85,7 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
   const int tiles = (T + 15) >> 4;
   int64_t b;
   int tile;
-  causal_block_tile(blockIdx.x, a.B, tiles, b, tile);
+  block_tile(blockIdx.x, a.B, tiles, a.pair_cus, b, tile);
 
   float* rows = smem;  // 16 score rows
   uint32_t* hist = reinterpret_cast<uint32_t*>(smem + 16 * RS) + wave * 256;
@@ -122,7 +145,9 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
     // threshold: k_eff-th largest of the full row, whose s > t entries are
     // -inf (dsa_attention.py:41-44).
     const int n = t + 1;
-    const float thr = (n < a.keff) ? -__builtin_huge_valf() : wave_select_kth(row, n, a.keff, hist);
+    const float thr = (n < a.keff) ? -__builtin_huge_valf()
+                                   : wave_select_kth_bins(row, n, a.keff, hist,
+                                                          reinterpret_cast<uint32_t*>(list));
     // attention over keys with score >= thr.
     attend_query<Tag, EK, EV>(
         Q, K, V, t, a.HQ, a.DQ, a.DV, a.scale_log2, thr,
@@ -150,8 +175,36 @@ hipError_t launch(const FusedArgs& a, hipStream_t stream) {
   }();
   (void)attr_set;
   const int64_t nblk = a.B * ((a.T + 15) / 16);
+  FusedArgs args = a;
+  args.pair_cus = 0;
+  // CU count and resident blocks per CU of this instance at this LDS size
+  // (host queries, cached per thread for the last device and size seen).
+  thread_local int c_dev = -1, c_cus = 0, c_per_cu = 0;
+  thread_local size_t c_lds = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    if (dev != c_dev || lds != c_lds) {
+      int cus = 0, per_cu = 0;
+      if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+          hipOccupancyMaxActiveBlocksPerMultiprocessor(
+              &per_cu, reinterpret_cast<const void*>(kern), 64 * kFusedWaves, lds) == hipSuccess) {
+        c_dev = dev;
+        c_lds = lds;
+        c_cus = cus;
+        c_per_cu = per_cu;
+      } else {
+        (void)hipGetLastError();  // the default order needs neither figure
+        c_dev = -1;
+        c_cus = c_per_cu = 0;
+      }
+    }
+    if (c_per_cu == 2 && nblk > c_cus && nblk <= 2 * static_cast<int64_t>(c_cus) && c_cus % a.B == 0)
+      args.pair_cus = c_cus;
+  } else {
+    (void)hipGetLastError();
+  }
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(nblk)), dim3(64 * kFusedWaves), lds, stream,
-                     a);
+                     args);
   return hipGetLastError();
 }
 
@@ -178,7 +231,7 @@ hipError_t launch_fused(const void* qi, const void* ki, const void* wi, const vo
   if (B == 0 || T == 0) return hipSuccess;
   const int keff = top_k < T ? top_k : static_cast<int>(T);
   FusedArgs a{qi, ki, wi, Q, K, V, B, static_cast<int>(T), HI, HQ, DQ, DV, keff,
-              scale * 1.4426950408889634f, out, row_stride(static_cast<int>(T))};
+              scale * 1.4426950408889634f, out, row_stride(static_cast<int>(T)), 0};
   const int EK = elems_per_lane(HQ, DQ);
   if (elems_per_lane(HQ, DV) != EK) return hipErrorNotSupported;
   if (dtype == 0) {

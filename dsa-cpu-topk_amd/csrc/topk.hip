@@ -553,14 +553,6 @@ constexpr int kBrBins = 1024;    // sample histogram: value bins over the sample
 constexpr int kFinBins = 256;    // finishing wave's value bins over the kept values
 constexpr int kFinGather = 64;   // kept values of one finishing bin ranked in registers
 
-// Bin of v among top + 1 bins linear in value: (v - lo) * scale clamped to
-// [0, top].  For finite lo and scale >= 0 it is monotone non-decreasing in v
-// (each rounding step is monotone, then a clamp and a truncation), and -0
-// and +0 share a bin.
-__device__ __forceinline__ int value_bin(float v, float lo, float scale, float top) {
-  return static_cast<int>(__builtin_amdgcn_fmed3f((v - lo) * scale, 0.0f, top));
-}
-
 // A sample of four 4*NT-entry chunks spread evenly over the row is held in
 // registers and ranked approximately: one LDS histogram over kBrBins bins
 // linear in VALUE between the sample's minimum and maximum (bins follow the

@@ -1,4 +1,6 @@
 // wave_select.h -- k-th largest of one LDS-resident score row, one wave.
+// (wave_select_kth_bins, at the end, is the usual entry; wave_select_kth is
+// its exact fallback.)
 //
 // Replaces the fused reference kernel's tl.sort(...)[TOP_K-1]
 // (dsa_attention.py:151-155): same value (the k-th largest counting ties)
@@ -81,6 +83,100 @@ __device__ __forceinline__ float wave_select_kth(const float* row, int n, int k,
     }
   }
   return key_to_float(prefix);
+}
+
+// Same contract, usually in three reads of the row instead of four or more:
+// the row's min and max, a 256-bin histogram linear in value between them
+// (bins follow the data's density, so its ds_adds rarely collide), then the
+// few values of the bin holding the k-th largest are gathered into `gl` (64
+// words of wave-private LDS) and ranked against each other in registers:
+// the wanted one has fewer than k' greater and at least k' greater or equal.
+// Rows with a non-finite value, and bins holding more than 64 values (heavy
+// ties), take wave_select_kth.  -0 is reported as +0, as the key order does.
+__device__ __forceinline__ float wave_select_kth_bins(const float* row, int n, int k,
+                                                      uint32_t* hist, uint32_t* gl) {
+  const int lane = lane_id();
+  float lo = __builtin_huge_valf(), hi = -__builtin_huge_valf();
+  bool bad = false;
+  for (int s = 4 * lane; s < n; s += 4 * kWave) {
+    const float4 f = *reinterpret_cast<const float4*>(row + s);
+    const float fv[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (s + c < n) {
+        lo = fminf(lo, fv[c]);
+        hi = fmaxf(hi, fv[c]);
+        bad = bad || !(fabsf(fv[c]) <= __FLT_MAX__);
+      }
+    }
+  }
+  if (ballot(bad) != 0u) return wave_select_kth(row, n, k, hist);
+  lo = wave_extreme_f32<false>(lo);
+  hi = wave_extreme_f32<true>(hi);
+  if (!(hi > lo)) return hi + 0.0f;  // one value
+  const float scale = 256.0f / (hi - lo);
+  if (!(scale <= __FLT_MAX__)) return wave_select_kth(row, n, k, hist);
+  reinterpret_cast<uint4*>(hist)[lane] = make_uint4(0u, 0u, 0u, 0u);
+  wave_lds_sync();
+  for (int s = 4 * lane; s < n; s += 4 * kWave) {
+    const float4 f = *reinterpret_cast<const float4*>(row + s);
+    const float fv[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (s + c < n) atomicAdd(&hist[value_bin(fv[c], lo, scale, 255.0f)], 1u);
+  }
+  wave_lds_sync();
+  const uint32_t krem = static_cast<uint32_t>(k);
+  const uint4 h4 = reinterpret_cast<const uint4*>(hist)[lane];
+  const uint32_t h[4] = {h4.x, h4.y, h4.z, h4.w};
+  const uint32_t local = h[0] + h[1] + h[2] + h[3];
+  const uint32_t incl = wave_inclusive_sum(local);
+  const uint32_t abv = wave_read_lane(incl, kWave - 1) - incl;  // values in higher lanes' bins
+  const bool here = abv < krem && abv + local >= krem;
+  uint32_t bsel = 0, brank = 0, bcnt = 0;
+  if (here) {
+    uint32_t cum = abv;
+#pragma unroll
+    for (int i = 3; i >= 0; --i) {
+      if (bcnt == 0u && cum + h[i] >= krem) {
+        bsel = 4u * lane + i;
+        brank = krem - cum;
+        bcnt = h[i];
+      }
+      cum += h[i];
+    }
+  }
+  const int src = __ffsll(static_cast<unsigned long long>(ballot(here))) - 1;
+  bsel = wave_read_lane(bsel, src);
+  brank = wave_read_lane(brank, src);
+  bcnt = wave_read_lane(bcnt, src);
+  wave_lds_sync();  // histogram reads done (the fallback clears it)
+  if (bcnt > static_cast<uint32_t>(kWave)) return wave_select_kth(row, n, k, hist);
+  uint32_t ng = 0;
+  for (int s = 4 * lane; s < n; s += 4 * kWave) {
+    const float4 f = *reinterpret_cast<const float4*>(row + s);
+    const float fv[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bool in = s + c < n && value_bin(fv[c], lo, scale, 255.0f) == static_cast<int>(bsel);
+      const uint64_t m = ballot(in);
+      if (in) gl[ng + lanes_below(m)] = __float_as_uint(fv[c]);
+      ng += popc64(m);
+    }
+  }
+  wave_lds_sync();
+  const float mv = lane < static_cast<int>(bcnt) ? __uint_as_float(gl[lane]) : 0.0f;
+  uint32_t gt = 0, ge = 0;
+  for (uint32_t j = 0; j < bcnt; ++j) {
+    const float o = __uint_as_float(gl[j]);
+    gt += (o > mv) ? 1u : 0u;
+    ge += (o >= mv) ? 1u : 0u;
+  }
+  const bool hit = lane < static_cast<int>(bcnt) && gt < brank && ge >= brank;
+  const float res = __int_as_float(
+      wave_read_lane(__float_as_int(mv), __ffsll(static_cast<unsigned long long>(ballot(hit))) - 1));
+  wave_lds_sync();  // gather-list reads done before the caller reuses it
+  return res + 0.0f;
 }
 
 }  // namespace dsa

@@ -37,6 +37,26 @@ def test_fused_matches_oracle(dev, T, top_k, BLOCK_S):
     assert float((out.double() - ref).abs().max()) < 5e-4
 
 
+@pytest.mark.parametrize("T,top_k", [(256, 32), (512, 100)])
+def test_fused_tie_heavy_scores(dev, T, top_k):
+    """Integer-valued indexer inputs give exactly representable, heavily tied
+    scores (the same in fp32 and float64), so the fused kernel's in-LDS
+    select must keep exactly the oracle's tied set; batch element 1 has all
+    scores 0 (one value in every row)."""
+    g = torch.Generator().manual_seed(T)
+    B, HI, DI, HQ, DH = 2, 4, 32, 4, 32
+    qi = torch.randint(-1, 2, (B, T, HI, DI), generator=g).float()
+    ki = torch.randint(-1, 2, (B, T, DI), generator=g).float()
+    wi = torch.randint(1, 3, (B, T, HI), generator=g).float()
+    qi[1] = 0.0
+    Q, K, V = (torch.randn((B, T, HQ, DH), generator=g) for _ in range(3))
+    ins = (qi, ki, wi, Q, K, V)
+    say(f"fused tie-heavy T={T} k={top_k}")
+    out = D.dsa_fused_hip(*to_dev(ins, dev), top_k).cpu()
+    ref = O.dsa_forward(*ins, top_k)
+    assert float((out.double() - ref).abs().max()) < 5e-4
+
+
 def test_all_three_agree_small(dev):
     """test_dsa.py:44-52: naive / oracle / fused at HI=2, DI=16, HQ=2, D=16."""
     ins = ref_make(B=2, T=32, HI=2, DI=16, HQ=2, DQ=16, DV=16)
