@@ -17,7 +17,9 @@
 //
 // LDS per block: 16 score rows of RS floats, RS = round_up(T,32) + 16 (the
 // +16 puts consecutive rows on different banks for the MFMA epilogue
-// stores), plus a 256-bin histogram and a 512-entry key list per wave.
+// stores), plus a 256-bin histogram and a 512-entry key list per wave, and
+// each row's score range (min, max, non-finite flag per key half), which the
+// indexer's epilogue gathers so that the select starts at its histogram.
 #include "attn_tile.h"
 #include "dsa_launch.h"
 #include "indexer_tile.h"
@@ -66,9 +68,12 @@ __device__ __forceinline__ void block_tile(uint32_t bid, int64_t B, int tiles, i
   }
 }
 constexpr int kFusedWaves = 8;
+// Per (row, key half): the minimum, maximum and non-finite flag of the row's
+// causal scores, gathered by the indexer for the select.
+constexpr int kRangeWords = 16 * 2 * 3;
 size_t fused_lds_bytes(int T) {
   return static_cast<size_t>(16) * row_stride(T) * 4 + kFusedWaves * 256 * 4 +
-         kFusedWaves * kListCap * 4;
+         kFusedWaves * kListCap * 4 + kRangeWords * 4;
 }
 
 // Narrow indexer rows (DI <= 64) ask for 4 waves per SIMD (<= 128 VGPRs): the
@@ -90,6 +95,7 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
   float* rows = smem;  // 16 score rows
   uint32_t* hist = reinterpret_cast<uint32_t*>(smem + 16 * RS) + wave * 256;
   int* list = reinterpret_cast<int*>(smem + 16 * RS + kFusedWaves * 256) + wave * kListCap;
+  float* rng = smem + 16 * RS + kFusedWaves * 256 + kFusedWaves * kListCap;
 
   const raw* qi = static_cast<const raw*>(a.qi) + b * T * static_cast<int64_t>(a.HI) * DI;
   const raw* ki = static_cast<const raw*>(a.ki) + b * T * static_cast<int64_t>(DI);
@@ -108,6 +114,8 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
       const int s_lo = half == 0 ? 0 : mid;
       const int s_hi = half == 0 ? (mid < s_end ? mid : s_end) : s_end;
       float* qrows = rows + quad * 4 * RS;
+      const int qrow = tq + g;  // the query of this lane's scores
+      float lo = __builtin_huge_valf(), hi = -__builtin_huge_valf(), bad = 0.0f;
       if (s_lo < s_hi)
         indexer_rows<Tag, DI, KB>(qi, ki, wi, T, a.HI, static_cast<int64_t>(a.HI) * DI, DI,
                                   a.HI, tq, s_lo, s_hi,
@@ -116,8 +124,32 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
           for (int kb = 0; kb < KB; ++kb) {
             const int s = s0 + 16 * kb + r16;
             if (s < T) qrows[g * RS + s] = sc[kb];
+            if (s <= qrow && s < T) {
+              lo = fminf(lo, sc[kb]);
+              hi = fmaxf(hi, sc[kb]);
+              bad = fabsf(sc[kb]) <= __FLT_MAX__ ? bad : 1.0f;
+            }
           }
         });
+      // over the 16 lanes that hold this row's keys
+      lo = fminf(lo, dpp_partner<8>(lo));
+      lo = fminf(lo, dpp_partner<4>(lo));
+      lo = fminf(lo, dpp_partner<2>(lo));
+      lo = fminf(lo, dpp_partner<1>(lo));
+      hi = fmaxf(hi, dpp_partner<8>(hi));
+      hi = fmaxf(hi, dpp_partner<4>(hi));
+      hi = fmaxf(hi, dpp_partner<2>(hi));
+      hi = fmaxf(hi, dpp_partner<1>(hi));
+      bad = fmaxf(bad, dpp_partner<8>(bad));
+      bad = fmaxf(bad, dpp_partner<4>(bad));
+      bad = fmaxf(bad, dpp_partner<2>(bad));
+      bad = fmaxf(bad, dpp_partner<1>(bad));
+      if (r16 == 0) {
+        float* slot = rng + ((quad * 4 + g) * 2 + half) * 3;
+        slot[0] = lo;
+        slot[1] = hi;
+        slot[2] = bad;
+      }
     }
   }
   block_sync_lds();
@@ -145,9 +177,12 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
     // threshold: k_eff-th largest of the full row, whose s > t entries are
     // -inf (dsa_attention.py:41-44).
     const int n = t + 1;
+    const float* rr3 = rng + r * 6;  // the row's two key halves
     const float thr = (n < a.keff) ? -__builtin_huge_valf()
                                    : wave_select_kth_bins(row, n, a.keff, hist,
-                                                          reinterpret_cast<uint32_t*>(list));
+                                                          reinterpret_cast<uint32_t*>(list),
+                                                          fminf(rr3[0], rr3[3]), fmaxf(rr3[1], rr3[4]),
+                                                          rr3[2] != 0.0f || rr3[5] != 0.0f);
     // attention over keys with score >= thr.
     attend_query<Tag, EK, EV>(
         Q, K, V, t, a.HQ, a.DQ, a.DV, a.scale_log2, thr,
@@ -234,11 +269,14 @@ hipError_t launch_fused(const void* qi, const void* ki, const void* wi, const vo
               scale * 1.4426950408889634f, out, row_stride(static_cast<int>(T)), 0};
   const int EK = elems_per_lane(HQ, DQ);
   if (elems_per_lane(HQ, DV) != EK) return hipErrorNotSupported;
+  // Key blocks per indexer super-block (KB): fp32 rows take 2 (config 1:
+  // 34.0 us against 35.1 at 4 and 34.4 at 1), DI = 64 takes 1 to stay within
+  // 128 VGPRs without scratch.
   if (dtype == 0) {
     switch (DI) {
-      case 16: DSA_FUSED_EK(F32, 16, 4)
-      case 32: DSA_FUSED_EK(F32, 32, 4)
-      case 64: DSA_FUSED_EK(F32, 64, 4)
+      case 16: DSA_FUSED_EK(F32, 16, 2)
+      case 32: DSA_FUSED_EK(F32, 32, 2)
+      case 64: DSA_FUSED_EK(F32, 64, 1)
       case 128: DSA_FUSED_EK(F32, 128, 2)
     }
   } else if (dtype == 1) {

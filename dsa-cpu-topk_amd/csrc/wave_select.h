@@ -93,26 +93,13 @@ __device__ __forceinline__ float wave_select_kth(const float* row, int n, int k,
 // the wanted one has fewer than k' greater and at least k' greater or equal.
 // Rows with a non-finite value, and bins holding more than 64 values (heavy
 // ties), take wave_select_kth.  -0 is reported as +0, as the key order does.
+// With the row's minimum lo, maximum hi and whether it holds a non-finite
+// value (bad) already known (wave-uniform).
 __device__ __forceinline__ float wave_select_kth_bins(const float* row, int n, int k,
-                                                      uint32_t* hist, uint32_t* gl) {
+                                                      uint32_t* hist, uint32_t* gl, float lo,
+                                                      float hi, bool bad) {
   const int lane = lane_id();
-  float lo = __builtin_huge_valf(), hi = -__builtin_huge_valf();
-  bool bad = false;
-  for (int s = 4 * lane; s < n; s += 4 * kWave) {
-    const float4 f = *reinterpret_cast<const float4*>(row + s);
-    const float fv[4] = {f.x, f.y, f.z, f.w};
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if (s + c < n) {
-        lo = fminf(lo, fv[c]);
-        hi = fmaxf(hi, fv[c]);
-        bad = bad || !(fabsf(fv[c]) <= __FLT_MAX__);
-      }
-    }
-  }
-  if (ballot(bad) != 0u) return wave_select_kth(row, n, k, hist);
-  lo = wave_extreme_f32<false>(lo);
-  hi = wave_extreme_f32<true>(hi);
+  if (bad) return wave_select_kth(row, n, k, hist);
   if (!(hi > lo)) return hi + 0.0f;  // one value
   const float scale = 256.0f / (hi - lo);
   if (!(scale <= __FLT_MAX__)) return wave_select_kth(row, n, k, hist);
@@ -177,6 +164,27 @@ __device__ __forceinline__ float wave_select_kth_bins(const float* row, int n, i
       wave_read_lane(__float_as_int(mv), __ffsll(static_cast<unsigned long long>(ballot(hit))) - 1));
   wave_lds_sync();  // gather-list reads done before the caller reuses it
   return res + 0.0f;
+}
+
+__device__ __forceinline__ float wave_select_kth_bins(const float* row, int n, int k,
+                                                      uint32_t* hist, uint32_t* gl) {
+  const int lane = lane_id();
+  float lo = __builtin_huge_valf(), hi = -__builtin_huge_valf();
+  bool bad = false;
+  for (int s = 4 * lane; s < n; s += 4 * kWave) {
+    const float4 f = *reinterpret_cast<const float4*>(row + s);
+    const float fv[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (s + c < n) {
+        lo = fminf(lo, fv[c]);
+        hi = fmaxf(hi, fv[c]);
+        bad = bad || !(fabsf(fv[c]) <= __FLT_MAX__);
+      }
+    }
+  }
+  return wave_select_kth_bins(row, n, k, hist, gl, wave_extreme_f32<false>(lo),
+                              wave_extreme_f32<true>(hi), ballot(bad) != 0u);
 }
 
 }  // namespace dsa
