@@ -2,23 +2,23 @@
 //
 // Replaces _dsa_fused_kernel + dsa_attention_triton (reference
 // dsa_attention.py:96-227).  A block of 8 waves owns 16 consecutive queries:
-//   1. lightning indexer on MFMA: wave w computes the score rows of queries
-//      t0+4(w%4) .. +3 over one half (w/4) of their causal key range, into
-//      LDS rows shared by the block;
+//   1. lightning indexer on MFMA: wave w computes the score rows of 8 (DI <=
+//      32) or 4 queries over a quarter or a half of their causal key range,
+//      into LDS rows shared by the block;
 //   -- one block barrier --
 //   2. wave w takes rows 2w and 2w+1: the k_eff-th largest by a value-bin
 //      histogram (wave_select.h), then sparse attention over keys with score >= thr
 //      (attn_tile.h).
 // The score rows never touch HBM.  Splitting the indexer's key range over
-// wave pairs and giving each wave two rows (not four) doubles the waves that
-// hide the gathers' memory latency, at the same MFMA work.  Blocks run
+// several waves and giving each wave two rows (not four or eight) multiplies
+// the waves that hide the gathers' memory latency, at the same MFMA work.  Blocks run
 // longest queries first, spread evenly over the XCDs, or, when the grid is
 // resident two blocks per CU, one long and one short tile per CU (block_tile).
 //
 // LDS per block: 16 score rows of RS floats, RS = round_up(T,32) + 16 (the
 // +16 puts consecutive rows on different banks for the MFMA epilogue
 // stores), plus a 256-bin histogram and a 512-entry key list per wave, and
-// each row's score range (min, max, non-finite flag per key half), which the
+// each row's score range (min, max, non-finite flag per key part), which the
 // indexer's epilogue gathers so that the select starts at its histogram.
 #include "attn_tile.h"
 #include "dsa_launch.h"
@@ -68,9 +68,9 @@ __device__ __forceinline__ void block_tile(uint32_t bid, int64_t B, int tiles, i
   }
 }
 constexpr int kFusedWaves = 8;
-// Per (row, key half): the minimum, maximum and non-finite flag of the row's
-// causal scores, gathered by the indexer for the select.
-constexpr int kRangeWords = 16 * 2 * 3;
+// Per (row, key quarter): the minimum, maximum and non-finite flag of the
+// row's causal scores, gathered by the indexer for the select.
+constexpr int kRangeWords = 16 * 4 * 3;
 size_t fused_lds_bytes(int T) {
   return static_cast<size_t>(16) * row_stride(T) * 4 + kFusedWaves * 256 * 4 +
          kFusedWaves * kListCap * 4 + kRangeWords * 4;
@@ -101,54 +101,81 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
   const raw* ki = static_cast<const raw*>(a.ki) + b * T * static_cast<int64_t>(DI);
   const raw* wi = static_cast<const raw*>(a.wi) + b * T * static_cast<int64_t>(a.HI);
 
-  // 1. indexer rows tq..tq+3 over keys [0, min(T, tq+4)), split in two
-  //    halves of whole super-blocks between waves w and w+4.
+  // 1. indexer: the block's 16 queries in groups of 4*QGN, each group's
+  //    causal key range [0, min(T, tg + 4*QGN)) split into NPART parts of
+  //    whole super-blocks; wave w takes group w % NGRP and part w / NGRP.
+  //    Narrow rows (DI <= 32, attention slices of <= 4 elements per lane)
+  //    take 8-query groups, so every key block a wave loads serves 8
+  //    queries; the others keep 4-query groups within 128 VGPRs.
+  constexpr int QGN = (DI <= 32 && EK <= 4) ? 2 : 1;  // 4-query groups per wave
+  constexpr int NGRP = 4 / QGN;          // query groups per block
+  constexpr int NPART = kFusedWaves / NGRP;
   {
-    const int quad = wave & 3, half = wave >> 2;
-    const int tq = tile * 16 + quad * 4;
-    if (tq < T) {
+    const int grp = wave % NGRP, part = wave / NGRP;
+    const int tg = tile * 16 + grp * 4 * QGN;
+    if (tg < T) {
       constexpr int SB = 16 * KB;
-      const int s_end = (tq + 4 < T) ? tq + 4 : T;
+      const int s_end = (tg + 4 * QGN < T) ? tg + 4 * QGN : T;
       const int nsb = (s_end + SB - 1) / SB;
-      const int mid = (nsb / 2) * SB;
-      const int s_lo = half == 0 ? 0 : mid;
-      const int s_hi = half == 0 ? (mid < s_end ? mid : s_end) : s_end;
-      float* qrows = rows + quad * 4 * RS;
-      const int qrow = tq + g;  // the query of this lane's scores
-      float lo = __builtin_huge_valf(), hi = -__builtin_huge_valf(), bad = 0.0f;
-      if (s_lo < s_hi)
-        indexer_rows<Tag, DI, KB>(qi, ki, wi, T, a.HI, static_cast<int64_t>(a.HI) * DI, DI,
-                                  a.HI, tq, s_lo, s_hi,
-                                  [&](int s0, const float(&sc)[KB]) {
+      const int s_lo = ((part * nsb) / NPART) * SB;
+      const int s_hi = min(((part + 1) * nsb / NPART) * SB, s_end);
+      float lo[QGN], hi[QGN], bad[QGN];
 #pragma unroll
-          for (int kb = 0; kb < KB; ++kb) {
-            const int s = s0 + 16 * kb + r16;
-            if (s < T) qrows[g * RS + s] = sc[kb];
-            if (s <= qrow && s < T) {
-              lo = fminf(lo, sc[kb]);
-              hi = fmaxf(hi, sc[kb]);
-              bad = fabsf(sc[kb]) <= __FLT_MAX__ ? bad : 1.0f;
-            }
+      for (int qg = 0; qg < QGN; ++qg) {
+        lo[qg] = __builtin_huge_valf();
+        hi[qg] = -__builtin_huge_valf();
+        bad[qg] = 0.0f;
+      }
+      auto take = [&](int qg, int s0, const float (&sc)[KB]) {
+        float* qrow_p = rows + (grp * 4 * QGN + qg * 4 + g) * RS;
+        const int qrow = tg + qg * 4 + g;  // the query of these scores
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          const int s = s0 + 16 * kb + r16;
+          const float v = sc[kb];
+          if (s < T) qrow_p[s] = v;
+          if (s <= qrow && s < T) {
+            lo[qg] = fminf(lo[qg], v);
+            hi[qg] = fmaxf(hi[qg], v);
+            bad[qg] = fabsf(v) <= __FLT_MAX__ ? bad[qg] : 1.0f;
           }
-        });
-      // over the 16 lanes that hold this row's keys
-      lo = fminf(lo, dpp_partner<8>(lo));
-      lo = fminf(lo, dpp_partner<4>(lo));
-      lo = fminf(lo, dpp_partner<2>(lo));
-      lo = fminf(lo, dpp_partner<1>(lo));
-      hi = fmaxf(hi, dpp_partner<8>(hi));
-      hi = fmaxf(hi, dpp_partner<4>(hi));
-      hi = fmaxf(hi, dpp_partner<2>(hi));
-      hi = fmaxf(hi, dpp_partner<1>(hi));
-      bad = fmaxf(bad, dpp_partner<8>(bad));
-      bad = fmaxf(bad, dpp_partner<4>(bad));
-      bad = fmaxf(bad, dpp_partner<2>(bad));
-      bad = fmaxf(bad, dpp_partner<1>(bad));
-      if (r16 == 0) {
-        float* slot = rng + ((quad * 4 + g) * 2 + half) * 3;
-        slot[0] = lo;
-        slot[1] = hi;
-        slot[2] = bad;
+        }
+      };
+      if (s_lo < s_hi) {
+        if constexpr (QGN == 1) {
+          indexer_rows<Tag, DI, KB, 1>(qi, ki, wi, T, a.HI, static_cast<int64_t>(a.HI) * DI, DI,
+                                       a.HI, tg, s_lo, s_hi,
+                                       [&](int s0, const float(&sc)[KB]) { take(0, s0, sc); });
+        } else {
+          indexer_rows<Tag, DI, KB, QGN>(qi, ki, wi, T, a.HI, static_cast<int64_t>(a.HI) * DI,
+                                         DI, a.HI, tg, s_lo, s_hi,
+                                         [&](int s0, const float(&sc)[QGN][KB]) {
+#pragma unroll
+                                           for (int qg = 0; qg < QGN; ++qg) take(qg, s0, sc[qg]);
+                                         });
+        }
+      }
+      // over the 16 lanes that hold each row's keys
+#pragma unroll
+      for (int qg = 0; qg < QGN; ++qg) {
+        lo[qg] = fminf(lo[qg], dpp_partner<8>(lo[qg]));
+        lo[qg] = fminf(lo[qg], dpp_partner<4>(lo[qg]));
+        lo[qg] = fminf(lo[qg], dpp_partner<2>(lo[qg]));
+        lo[qg] = fminf(lo[qg], dpp_partner<1>(lo[qg]));
+        hi[qg] = fmaxf(hi[qg], dpp_partner<8>(hi[qg]));
+        hi[qg] = fmaxf(hi[qg], dpp_partner<4>(hi[qg]));
+        hi[qg] = fmaxf(hi[qg], dpp_partner<2>(hi[qg]));
+        hi[qg] = fmaxf(hi[qg], dpp_partner<1>(hi[qg]));
+        bad[qg] = fmaxf(bad[qg], dpp_partner<8>(bad[qg]));
+        bad[qg] = fmaxf(bad[qg], dpp_partner<4>(bad[qg]));
+        bad[qg] = fmaxf(bad[qg], dpp_partner<2>(bad[qg]));
+        bad[qg] = fmaxf(bad[qg], dpp_partner<1>(bad[qg]));
+        if (r16 == 0) {
+          float* slot = rng + ((grp * 4 * QGN + qg * 4 + g) * 4 + part) * 3;
+          slot[0] = lo[qg];
+          slot[1] = hi[qg];
+          slot[2] = bad[qg];
+        }
       }
     }
   }
@@ -177,12 +204,19 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
     // threshold: k_eff-th largest of the full row, whose s > t entries are
     // -inf (dsa_attention.py:41-44).
     const int n = t + 1;
-    const float* rr3 = rng + r * 6;  // the row's two key halves
+    const float* rq = rng + r * 12;  // the row's NPART key parts
+    float rlo = rq[0], rhi = rq[1], rb = rq[2];
+#pragma unroll
+    for (int p = 1; p < NPART; ++p) {
+      rlo = fminf(rlo, rq[3 * p]);
+      rhi = fmaxf(rhi, rq[3 * p + 1]);
+      rb = fmaxf(rb, rq[3 * p + 2]);
+    }
+    const bool rbad = rb != 0.0f;
     const float thr = (n < a.keff) ? -__builtin_huge_valf()
                                    : wave_select_kth_bins(row, n, a.keff, hist,
                                                           reinterpret_cast<uint32_t*>(list),
-                                                          fminf(rr3[0], rr3[3]), fmaxf(rr3[1], rr3[4]),
-                                                          rr3[2] != 0.0f || rr3[5] != 0.0f);
+                                                          rlo, rhi, rbad);
     // attention over keys with score >= thr.
     attend_query<Tag, EK, EV>(
         Q, K, V, t, a.HQ, a.DQ, a.DV, a.scale_log2, thr,

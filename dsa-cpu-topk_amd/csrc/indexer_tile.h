@@ -94,15 +94,17 @@ struct Slice<FP8, E> {
   }
 };
 
-// Computes scores of queries t0..t0+3 (batch row base pointers given) against
-// keys [s_begin, s_end) in super-blocks of 16*KB keys and hands each finished
-// super-block to sink(s0, sc) where lane l holds sc[kb] = score of query
-// t0 + l/16 and key s0 + 16*kb + l%16.  Entries with key > query, key >= T or
-// query >= T hold garbage/-inf; the sink applies the causal mask and bounds.
+// Computes scores of queries t0..t0+4*QG-1 (batch row base pointers given)
+// against keys [s_begin, s_end) in super-blocks of 16*KB keys and hands each
+// finished super-block to sink(s0, sc) where lane l holds sc[qg][kb] = score
+// of query t0 + 4*qg + l/16 and key s0 + 16*kb + l%16 (for QG = 1, sc[kb]).
+// Entries with key > query, key >= T or query >= T hold garbage/-inf; the
+// sink applies the causal mask and bounds.  QG query groups of 4 share every
+// key block a wave loads, so QG = 2 halves the key loads per query.
 //
 // q : [T, HI, DI] of this batch element   k : [T, DI]   w : [T, HI], rows of
 // consecutive tokens ldq / ldk / ldw elements apart.
-template <typename Tag, int DI, int KB, typename Sink>
+template <typename Tag, int DI, int KB, int QG = 1, typename Sink>
 __device__ __forceinline__ void indexer_rows(const typename Tag::raw* __restrict__ q,
                                              const typename Tag::raw* __restrict__ k,
                                              const typename Tag::raw* __restrict__ w, int T,
@@ -115,16 +117,13 @@ __device__ __forceinline__ void indexer_rows(const typename Tag::raw* __restrict
   const int r16 = lane & 15; // A row / B column
   const int nhg = (HI + 3) >> 2;
 
-  // A row of this lane: query t0 + r16/4, head 4*hg + r16%4.
-  const int qa = t0 + (r16 >> 2);
+  // A row of this lane in query group qg: query t0 + 4qg + r16/4, head
+  // 4*hg + r16%4; output query t0 + 4qg + g.
   const int ha = r16 & 3;
-  // Output query of this lane.
-  const int qo = t0 + g;
 
-  // Head-group-invariant operands when HI <= 4: load once.
-  S a_cached;
-  float w_cached[4];
-  auto load_a = [&](int hg, S& a, float (&wv)[4]) {
+  auto load_a = [&](int qg, int hg, S& a, float (&wv)[4]) {
+    const int qa = t0 + 4 * qg + (r16 >> 2);
+    const int qo = t0 + 4 * qg + g;
     const int head = 4 * hg + ha;
     if (qa < T && head < HI)
       a.load(q + static_cast<int64_t>(qa) * ldq + head * DI + g * E);
@@ -136,7 +135,13 @@ __device__ __forceinline__ void indexer_rows(const typename Tag::raw* __restrict
       wv[r] = (qo < T && hw < HI) ? to_f32(Tag{}, w[static_cast<int64_t>(qo) * ldw + hw]) : 0.f;
     }
   };
-  if (nhg == 1) load_a(0, a_cached, w_cached);
+  // Head-group-invariant operands when HI <= 4: load once.
+  S a_cached[QG];
+  float w_cached[QG][4];
+  if (nhg == 1) {
+#pragma unroll
+    for (int qg = 0; qg < QG; ++qg) load_a(qg, 0, a_cached[qg], w_cached[qg]);
+  }
 
   // Key blocks of super-block s0 -> registers.  The next super-block is
   // loaded while the MFMAs of the current one run.
@@ -155,35 +160,42 @@ __device__ __forceinline__ void indexer_rows(const typename Tag::raw* __restrict
   for (int s0 = s_begin; s0 < s_end; s0 += 16 * KB) {
     S bn[KB];
     if (s0 + 16 * KB < s_end) load_b(s0 + 16 * KB, bn);
-    float sc[KB];
+    float sc[QG][KB];
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) sc[kb] = 0.f;
+    for (int qg = 0; qg < QG; ++qg)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) sc[qg][kb] = 0.f;
 
     for (int hg = 0; hg < nhg; ++hg) {
-      S a;
-      float wv[4];
-      if (nhg == 1) {
-        a = a_cached;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) wv[r] = w_cached[r];
-      } else {
-        load_a(hg, a, wv);
-      }
-      f32x4 acc[KB];
+      for (int qg = 0; qg < QG; ++qg) {
+        S a;
+        float wv[4];
+        if (nhg == 1) {
+          a = a_cached[qg];
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) acc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int r = 0; r < 4; ++r) wv[r] = w_cached[qg][r];
+        } else {
+          load_a(qg, hg, a, wv);
+        }
+        f32x4 acc[KB];
 #pragma unroll
-      for (int i = 0; i < S::kSteps; ++i) {
+        for (int kb = 0; kb < KB; ++kb) acc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) acc[kb] = a.mfma(i, bk[kb], acc[kb]);
-      }
+        for (int i = 0; i < S::kSteps; ++i) {
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
+          for (int kb = 0; kb < KB; ++kb) acc[kb] = a.mfma(i, bk[kb], acc[kb]);
+        }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sc[kb] = fmaf(wv[r], fmaxf(acc[kb][r], 0.f), sc[kb]);
+        for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            sc[qg][kb] = fmaf(wv[r], fmaxf(acc[kb][r], 0.f), sc[qg][kb]);
+        }
       }
     }
-    sink(s0, sc);
+    if constexpr (QG == 1) sink(s0, sc[0]);
+    else sink(s0, sc);
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) bk[kb] = bn[kb];
   }
