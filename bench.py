@@ -549,7 +549,7 @@ def main():
                      "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 5),
                      "traffic": traffic_from_profile(),
-                     "kernel": "fused_kernel<F32,32,4,2,2>",
+                     "kernel": "fused_kernel<F32,32,2,2,2,16>",
                      "kernel_ms": round(kern_s * 1e3, 5),
                      "flops_per_launch": flops},
         "split": {"ms_per_step": round(split_s * 1e3, 5),

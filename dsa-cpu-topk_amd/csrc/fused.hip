@@ -1,21 +1,23 @@
 // fused.hip -- whole DSA forward in one kernel for T <= 2048 (gfx950).
 //
 // Replaces _dsa_fused_kernel + dsa_attention_triton (reference
-// dsa_attention.py:96-227).  A block of 8 waves owns 16 consecutive queries:
-//   1. lightning indexer on MFMA: wave w computes the score rows of 8 (DI <=
-//      32) or 4 queries over a quarter or a half of their causal key range,
-//      into LDS rows shared by the block;
+// dsa_attention.py:96-227).  A block of 8 waves owns QB = 16 consecutive
+// queries (8 when 16-query blocks would leave compute units idle):
+//   1. lightning indexer on MFMA: each wave computes the score rows of 8
+//      (DI <= 32) or 4 queries over a part of their causal key range, into
+//      LDS rows shared by the block;
 //   -- one block barrier --
-//   2. wave w takes rows 2w and 2w+1: the k_eff-th largest by a value-bin
-//      histogram (wave_select.h), then sparse attention over keys with score >= thr
-//      (attn_tile.h).
+//   2. each wave takes QB/8 rows: the k_eff-th largest by a value-bin
+//      histogram (wave_select.h), then sparse attention over keys with
+//      score >= thr (attn_tile.h).
 // The score rows never touch HBM.  Splitting the indexer's key range over
-// several waves and giving each wave two rows (not four or eight) multiplies
-// the waves that hide the gathers' memory latency, at the same MFMA work.  Blocks run
+// several waves and giving each wave one or two rows multiplies the waves
+// that hide the gathers' memory latency, at the same MFMA work.  Blocks run
 // longest queries first, spread evenly over the XCDs, or, when the grid is
-// resident two blocks per CU, one long and one short tile per CU (block_tile).
+// resident two blocks per CU, one long and one short tile per CU
+// (block_tile).
 //
-// LDS per block: 16 score rows of RS floats, RS = round_up(T,32) + 16 (the
+// LDS per block: QB score rows of RS floats, RS = round_up(T,32) + 16 (the
 // +16 puts consecutive rows on different banks for the MFMA epilogue
 // stores), plus a 256-bin histogram and a 512-entry key list per wave, and
 // each row's score range (min, max, non-finite flag per key part), which the
@@ -68,18 +70,23 @@ __device__ __forceinline__ void block_tile(uint32_t bid, int64_t B, int tiles, i
   }
 }
 constexpr int kFusedWaves = 8;
-// Per (row, key quarter): the minimum, maximum and non-finite flag of the
-// row's causal scores, gathered by the indexer for the select.
-constexpr int kRangeWords = 16 * 4 * 3;
-size_t fused_lds_bytes(int T) {
-  return static_cast<size_t>(16) * row_stride(T) * 4 + kFusedWaves * 256 * 4 +
+// Per (row, key part): the minimum, maximum and non-finite flag of the
+// row's causal scores, gathered by the indexer for the select (rows x parts
+// is at most 64).
+constexpr int kRangeWords = 64 * 3;
+size_t fused_lds_bytes(int T, int QB) {
+  return static_cast<size_t>(QB) * row_stride(T) * 4 + kFusedWaves * 256 * 4 +
          kFusedWaves * kListCap * 4 + kRangeWords * 4;
 }
 
 // Narrow indexer rows (DI <= 64) ask for 4 waves per SIMD (<= 128 VGPRs): the
 // whole grid of a T = 512 problem is then resident at once.
-template <typename Tag, int DI, int KB, int EK, int EV>
+// QB queries per block (16, or 8 when 16-query blocks would leave CUs idle):
+// each wave finishes QB/8 rows.
+template <typename Tag, int DI, int KB, int EK, int EV, int QB>
 __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kernel(FusedArgs a) {
+  static_assert(QB == 8 || QB == 16, "8 or 16 queries per block");
+  constexpr int RPW = QB / kFusedWaves;  // rows per wave
   using raw = typename Tag::raw;
   extern __shared__ __align__(16) float smem[];
   const int wave = threadIdx.x >> 6;
@@ -87,32 +94,32 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
   const int g = lane >> 4, r16 = lane & 15;
   const int T = a.T;
   const int RS = a.RS;
-  const int tiles = (T + 15) >> 4;
+  const int tiles = (T + QB - 1) / QB;
   int64_t b;
   int tile;
   block_tile(blockIdx.x, a.B, tiles, a.pair_cus, b, tile);
 
-  float* rows = smem;  // 16 score rows
-  uint32_t* hist = reinterpret_cast<uint32_t*>(smem + 16 * RS) + wave * 256;
-  int* list = reinterpret_cast<int*>(smem + 16 * RS + kFusedWaves * 256) + wave * kListCap;
-  float* rng = smem + 16 * RS + kFusedWaves * 256 + kFusedWaves * kListCap;
+  float* rows = smem;  // QB score rows
+  uint32_t* hist = reinterpret_cast<uint32_t*>(smem + QB * RS) + wave * 256;
+  int* list = reinterpret_cast<int*>(smem + QB * RS + kFusedWaves * 256) + wave * kListCap;
+  float* rng = smem + QB * RS + kFusedWaves * 256 + kFusedWaves * kListCap;
 
   const raw* qi = static_cast<const raw*>(a.qi) + b * T * static_cast<int64_t>(a.HI) * DI;
   const raw* ki = static_cast<const raw*>(a.ki) + b * T * static_cast<int64_t>(DI);
   const raw* wi = static_cast<const raw*>(a.wi) + b * T * static_cast<int64_t>(a.HI);
 
-  // 1. indexer: the block's 16 queries in groups of 4*QGN, each group's
+  // 1. indexer: the block's QB queries in groups of 4*QGN, each group's
   //    causal key range [0, min(T, tg + 4*QGN)) split into NPART parts of
   //    whole super-blocks; wave w takes group w % NGRP and part w / NGRP.
   //    Narrow rows (DI <= 32, attention slices of <= 4 elements per lane)
   //    take 8-query groups, so every key block a wave loads serves 8
   //    queries; the others keep 4-query groups within 128 VGPRs.
   constexpr int QGN = (DI <= 32 && EK <= 4) ? 2 : 1;  // 4-query groups per wave
-  constexpr int NGRP = 4 / QGN;          // query groups per block
+  constexpr int NGRP = QB / (4 * QGN);   // query groups per block
   constexpr int NPART = kFusedWaves / NGRP;
   {
     const int grp = wave % NGRP, part = wave / NGRP;
-    const int tg = tile * 16 + grp * 4 * QGN;
+    const int tg = tile * QB + grp * 4 * QGN;
     if (tg < T) {
       constexpr int SB = 16 * KB;
       const int s_end = (tg + 4 * QGN < T) ? tg + 4 * QGN : T;
@@ -171,7 +178,7 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
         bad[qg] = fmaxf(bad[qg], dpp_partner<2>(bad[qg]));
         bad[qg] = fmaxf(bad[qg], dpp_partner<1>(bad[qg]));
         if (r16 == 0) {
-          float* slot = rng + ((grp * 4 * QGN + qg * 4 + g) * 4 + part) * 3;
+          float* slot = rng + ((grp * 4 * QGN + qg * 4 + g) * NPART + part) * 3;
           slot[0] = lo[qg];
           slot[1] = hi[qg];
           slot[2] = bad[qg];
@@ -189,22 +196,22 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
 
   // 2. rows 2w, 2w+1 of the block.  Both query rows are loaded first, so
   // their latency hides behind the first row's select.
-  float qpre[2][EK];
+  float qpre[RPW][EK];
 #pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    const int t = min(tile * 16 + 2 * wave + rr, T - 1);
+  for (int rr = 0; rr < RPW; ++rr) {
+    const int t = min(tile * QB + RPW * wave + rr, T - 1);
     load_query<Tag, EK>(Q, t, static_cast<int>(EQ), a.scale_log2, qpre[rr]);
   }
 #pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    const int r = 2 * wave + rr;
-    const int t = tile * 16 + r;
+  for (int rr = 0; rr < RPW; ++rr) {
+    const int r = RPW * wave + rr;
+    const int t = tile * QB + r;
     if (t >= T) break;
     const float* row = rows + r * RS;
     // threshold: k_eff-th largest of the full row, whose s > t entries are
     // -inf (dsa_attention.py:41-44).
     const int n = t + 1;
-    const float* rq = rng + r * 12;  // the row's NPART key parts
+    const float* rq = rng + r * NPART * 3;  // the row's NPART key parts
     float rlo = rq[0], rhi = rq[1], rb = rq[2];
 #pragma unroll
     for (int p = 1; p < NPART; ++p) {
@@ -228,50 +235,63 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
   }
 }
 
-template <typename Tag, int DI, int KB, int EK, int EV>
+// Compute units of the current device (cached per thread), 0 if unknown.
+int device_cus() {
+  thread_local int c_dev = -1, c_cus = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  if (dev != c_dev) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      return 0;
+    }
+    c_dev = dev;
+    c_cus = cus;
+  }
+  return c_cus;
+}
+
+template <typename Tag, int DI, int KB, int EK, int EV, int QB>
 hipError_t launch(const FusedArgs& a, hipStream_t stream) {
-  const size_t lds = fused_lds_bytes(a.T);
-  auto kern = fused_kernel<Tag, DI, KB, EK, EV>;
+  const size_t lds = fused_lds_bytes(a.T, QB);
+  auto kern = fused_kernel<Tag, DI, KB, EK, EV, QB>;
   // Raise the dynamic-LDS limit of this instance once, to what T = 2048 needs.
   // A runtime that does not need (or know) the attribute may refuse it; the
   // launch below then reports any real shortfall itself.
   static const bool attr_set = [&] {
     const hipError_t e = hipFuncSetAttribute(
         reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-        static_cast<int>(fused_lds_bytes(static_cast<int>(kFusedMaxT))));
+        static_cast<int>(fused_lds_bytes(static_cast<int>(kFusedMaxT), QB)));
     if (e != hipSuccess) (void)hipGetLastError();
     return e == hipSuccess;
   }();
   (void)attr_set;
-  const int64_t nblk = a.B * ((a.T + 15) / 16);
+  const int64_t nblk = a.B * ((a.T + QB - 1) / QB);
   FusedArgs args = a;
   args.pair_cus = 0;
-  // CU count and resident blocks per CU of this instance at this LDS size
-  // (host queries, cached per thread for the last device and size seen).
-  thread_local int c_dev = -1, c_cus = 0, c_per_cu = 0;
+  // Resident blocks per CU of this instance at this LDS size (host query,
+  // cached per thread for the last device and size seen).
+  const int cus = device_cus();
+  thread_local int c_cus = 0, c_per_cu = 0;
   thread_local size_t c_lds = 0;
-  int dev = 0;
-  if (hipGetDevice(&dev) == hipSuccess) {
-    if (dev != c_dev || lds != c_lds) {
-      int cus = 0, per_cu = 0;
-      if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-          hipOccupancyMaxActiveBlocksPerMultiprocessor(
-              &per_cu, reinterpret_cast<const void*>(kern), 64 * kFusedWaves, lds) == hipSuccess) {
-        c_dev = dev;
-        c_lds = lds;
-        c_cus = cus;
-        c_per_cu = per_cu;
-      } else {
-        (void)hipGetLastError();  // the default order needs neither figure
-        c_dev = -1;
-        c_cus = c_per_cu = 0;
-      }
+  if (cus > 0 && (cus != c_cus || lds != c_lds)) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(kern), 64 * kFusedWaves, lds) != hipSuccess) {
+      (void)hipGetLastError();  // the default order needs no figure
+      per_cu = 0;
     }
-    if (c_per_cu == 2 && nblk > c_cus && nblk <= 2 * static_cast<int64_t>(c_cus) && c_cus % a.B == 0)
-      args.pair_cus = c_cus;
-  } else {
-    (void)hipGetLastError();
+    c_cus = cus;
+    c_lds = lds;
+    c_per_cu = per_cu;
   }
+  if (cus > 0 && c_per_cu == 2 && nblk > cus && nblk <= 2 * static_cast<int64_t>(cus) &&
+      cus % a.B == 0)
+    args.pair_cus = cus;
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(nblk)), dim3(64 * kFusedWaves), lds, stream,
                      args);
   return hipGetLastError();
@@ -282,12 +302,21 @@ int elems_per_lane(int HQ, int D) {
   return e < 1 ? 1 : e;
 }
 
+// 16-query blocks unless they would leave compute units idle (fewer blocks
+// than CUs): then 8-query blocks, one row per wave, twice the blocks.
+template <typename Tag, int DI, int KB, int EK>
+hipError_t launch_qb(const FusedArgs& a, hipStream_t stream) {
+  const int cus = device_cus();
+  if (cus > 0 && a.B * ((a.T + 15) / 16) < cus) return launch<Tag, DI, KB, EK, EK, 8>(a, stream);
+  return launch<Tag, DI, KB, EK, EK, 16>(a, stream);
+}
+
 #define DSA_FUSED_EK(Tag, di, kb)                                              \
   switch (EK) {                                                                \
-    case 1: return launch<Tag, di, kb, 1, 1>(a, stream);                       \
-    case 2: return launch<Tag, di, kb, 2, 2>(a, stream);                       \
-    case 4: return launch<Tag, di, kb, 4, 4>(a, stream);                       \
-    case 8: return launch<Tag, di, kb, 8, 8>(a, stream);                       \
+    case 1: return launch_qb<Tag, di, kb, 1>(a, stream);                       \
+    case 2: return launch_qb<Tag, di, kb, 2>(a, stream);                       \
+    case 4: return launch_qb<Tag, di, kb, 4>(a, stream);                       \
+    case 8: return launch_qb<Tag, di, kb, 8>(a, stream);                       \
   }                                                                            \
   break;
 
