@@ -44,8 +44,10 @@ __device__ __forceinline__ void load_query(const typename Tag::raw* __restrict__
 // Q/K/V point at this batch element: Q row t is Q + t*HQ*DQ, etc.
 // load4(s, sv) loads scores s..s+3 (s <= t, s % 4 == 0) of this query's row.
 // qpre: this lane's query slice from load_query, loaded early by the caller
-// (nullptr: loaded here).
-template <typename Tag, int EK, int EV, typename Load4>
+// (nullptr: loaded here).  PIPE: overlap each group's loads with the
+// neighbouring group's arithmetic (below); it needs more registers, which
+// the fused kernel has to spare and the gather kernel's occupancy does not.
+template <typename Tag, int EK, int EV, bool PIPE = false, typename Load4>
 __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict__ Q,
                                              const typename Tag::raw* __restrict__ K,
                                              const typename Tag::raw* __restrict__ V, int t,
@@ -77,50 +79,75 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
   float m = -__builtin_huge_valf();
   float lsum = 0.f;
 
-  // Keys gathered per round trip: as many as fit ~64 registers of K+V.
+  // Keys gathered per group: as many as fit ~64 registers of K+V.
   constexpr int U = (EK + EV <= 4) ? 16 : (EK + EV <= 8) ? 8 : (EK + EV <= 16) ? 4 : 2;
-  // Loads the K/V slices of keys ss[0..U) (entries past nu repeat key ss[0]
-  // and are ignored by the caller): the group's list entries come in with
-  // vector LDS reads, and every load takes a 32-bit byte offset against the
-  // uniform K or V base (the host keeps a batch element's K and V under
-  // 4 GiB), shared by K and V when their rows have the same length -- one
-  // offset register per key instead of two 64-bit addresses, so all of the
-  // group's loads fit in flight together.  No load is predicated: lanes past
-  // the row (EQ < 64*EK) read the row's start and contribute zero through
-  // q = 0 / an unstored accumulator.  One memory round trip per group.
+  // Loads the K (or V) slices of keys ss[0..U) (entries past nu repeat key
+  // ss[0] and are ignored by the caller): the group's list entries come in
+  // with vector LDS reads, and every load takes a 32-bit byte offset against
+  // the uniform K or V base (the host keeps a batch element's K and V under
+  // 4 GiB) -- one offset register per key, so all of a group's loads fit in
+  // flight together.  No load is predicated: lanes past the row
+  // (EQ < 64*EK) read the row's start and contribute zero through q = 0 / an
+  // unstored accumulator.
   constexpr uint32_t kRaw = sizeof(raw);
   const uint32_t koff_l = kact ? static_cast<uint32_t>(lane * EK) * kRaw : 0u;
   const uint32_t voff_l = vact ? static_cast<uint32_t>(lane * EV) * kRaw : 0u;
   const char* Kb = reinterpret_cast<const char*>(K);
   const char* Vb = reinterpret_cast<const char*>(V);
-  auto load_group = [&](const int* ss, int nu, float (&kv)[U][EK], float (&vv)[U][EV]) {
-    int sidx[U];
+  auto group_keys = [&](const int* ss, int nu, uint32_t (&sidx)[U]) {
+    int raw_idx[U];
     if constexpr (U % 4 == 0) {
 #pragma unroll
       for (int i = 0; i < U / 4; ++i) {
         const int4 v4 = reinterpret_cast<const int4*>(ss)[i];
-        sidx[4 * i] = v4.x; sidx[4 * i + 1] = v4.y; sidx[4 * i + 2] = v4.z; sidx[4 * i + 3] = v4.w;
+        raw_idx[4 * i] = v4.x; raw_idx[4 * i + 1] = v4.y; raw_idx[4 * i + 2] = v4.z; raw_idx[4 * i + 3] = v4.w;
       }
     } else {
 #pragma unroll
-      for (int u = 0; u < U; ++u) sidx[u] = ss[u];
+      for (int u = 0; u < U; ++u) raw_idx[u] = ss[u];
     }
 #pragma unroll
+    for (int u = 0; u < U; ++u) sidx[u] = static_cast<uint32_t>(u < nu ? raw_idx[u] : raw_idx[0]);
+  };
+  auto load_k = [&](const int* ss, int nu, float (&kv)[U][EK]) {
+    uint32_t sidx[U];
+    group_keys(ss, nu, sidx);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      load_cvt<Tag, EK>(reinterpret_cast<const raw*>(
+                            Kb + (sidx[u] * (static_cast<uint32_t>(EQ) * kRaw) + koff_l)),
+                        kv[u]);
+  };
+  auto load_v = [&](const int* ss, int nu, float (&vv)[U][EV]) {
+    uint32_t sidx[U];
+    group_keys(ss, nu, sidx);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      load_cvt<Tag, EV>(reinterpret_cast<const raw*>(
+                            Vb + (sidx[u] * (static_cast<uint32_t>(EVt) * kRaw) + voff_l)),
+                        vv[u]);
+  };
+  auto load_kv = [&](const int* ss, int nu, float (&kv)[U][EK], float (&vv)[U][EV]) {
+    uint32_t sidx[U];
+    group_keys(ss, nu, sidx);
+#pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint32_t s = static_cast<uint32_t>(u < nu ? sidx[u] : sidx[0]);
-      const uint32_t rk = s * (static_cast<uint32_t>(EQ) * kRaw);
-      const uint32_t rv = (EQ == EVt) ? rk : s * (static_cast<uint32_t>(EVt) * kRaw);
+      const uint32_t rk = sidx[u] * (static_cast<uint32_t>(EQ) * kRaw);
+      const uint32_t rv = (EQ == EVt) ? rk : sidx[u] * (static_cast<uint32_t>(EVt) * kRaw);
       load_cvt<Tag, EK>(reinterpret_cast<const raw*>(Kb + (rk + koff_l)), kv[u]);
       load_cvt<Tag, EV>(reinterpret_cast<const raw*>(Vb + (rv + voff_l)), vv[u]);
     }
   };
-  // Processes keys ss[0..nu) (nu <= U): all their K/V rows are loaded before
-  // any is used, so a group costs one memory round trip.
-  auto process = [&](const int* ss, int nu) {
-    float kv[U][EK];
-    float vv[U][EV];
-    load_group(ss, nu, kv, vv);
-    float lg[U];
+  // Each group is two halves: logits and the softmax update from K (A), then
+  // the P*V accumulation from V (B).  With PIPE the loop below issues a
+  // group's V loads before its half A and the next group's K loads before
+  // its half B, so each load overlaps the other half's arithmetic and the
+  // other load's wait (the K slices are dead after half A).
+
+  // General form: per-key logits summed over the head's lanes.
+  float lg[U];
+  float mnew_g = 0.f;
+  auto half_a = [&](int nu, const float (&kv)[U][EK]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       float d = 0.f;
@@ -157,17 +184,20 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
     lsum *= alpha;
 #pragma unroll
     for (int e = 0; e < EV; ++e) acc[e] *= alpha;
+    m = mnew;
+    mnew_g = mnew;
+  };
+  auto half_b = [&](int nu, const float (&vv)[U][EV]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (u < nu) {
         // bare v_exp_f32: results below 2^-126 flush to 0, which no sum can see
-        const float p = __builtin_amdgcn_exp2f(lg[u] - mnew);
+        const float p = __builtin_amdgcn_exp2f(lg[u] - mnew_g);
         lsum += p;
 #pragma unroll
         for (int e = 0; e < EV; ++e) acc[e] = fmaf(p, vv[u][e], acc[e]);
       }
     }
-    m = mnew;
   };
 
   // Variant for heads spanning exactly U lanes (K and V slices on the same
@@ -177,10 +207,8 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
   // probabilities are broadcast back for the P*V accumulation.  The
   // per-lane normaliser holds only the lane's own keys until the end.
   float lpart = 0.f;
-  auto process_rs = [&](const int* ss, int nu) {
-    float kv[U][EK];
-    float vv[U][EV];
-    load_group(ss, nu, kv, vv);
+  float p_own = 0.f;
+  auto half_a_rs = [&](int nu, const float (&kv)[U][EK]) {
     float v[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -210,18 +238,21 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
     rs_step(std::integral_constant<int, 2>{});
     rs_step(std::integral_constant<int, 1>{});
     const int j = lane & (U - 1);
-    const float lg = (j < nu) ? v[0] : -__builtin_huge_valf();
-    float mx = lg;
+    const float lgj = (j < nu) ? v[0] : -__builtin_huge_valf();
+    float mx = lgj;
     if constexpr (U > 1) mx = fmaxf(mx, dpp_partner<1>(mx));
     if constexpr (U > 2) mx = fmaxf(mx, dpp_partner<2>(mx));
     if constexpr (U > 4) mx = fmaxf(mx, dpp_partner<4>(mx));
     if constexpr (U > 8) mx = fmaxf(mx, dpp_partner<8>(mx));
     const float mnew = fmaxf(m, mx);
     const float alpha = exp2f(m - mnew);
-    const float p_own = (j < nu) ? __builtin_amdgcn_exp2f(lg - mnew) : 0.f;
+    p_own = (j < nu) ? __builtin_amdgcn_exp2f(lgj - mnew) : 0.f;
     lpart = fmaf(lpart, alpha, p_own);
 #pragma unroll
     for (int e = 0; e < EV; ++e) acc[e] *= alpha;
+    m = mnew;
+  };
+  auto half_b_rs = [&](int nu, const float (&vv)[U][EV]) {
     auto bcast_acc = [&](auto uc) {
       constexpr int UU = decltype(uc)::value;
       if constexpr (UU < U) {
@@ -235,10 +266,35 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
     [&]<int... Us>(std::integer_sequence<int, Us...>) {
       (bcast_acc(std::integral_constant<int, Us>{}), ...);
     }(std::make_integer_sequence<int, 16>{});
-    m = mnew;
   };
   // reduce-scatter needs every lane active on both sides (EQ = EVt = 64*E)
   const bool use_rs = same_map && lphk == U && EK == EV && EQ == kWave * EK && EVt == kWave * EV;
+
+  // All groups of one list segment.  PIPE: K of the first group, then per
+  // group V loads, half A, the next group's K loads, half B.  Otherwise a
+  // group's K and V loads, then both halves: one memory round trip each.
+  float kv[U][EK];
+  float vv[U][EV];
+  auto run_groups = [&](int total, auto&& ha, auto&& hb) {
+    if (total <= 0) return;
+    if constexpr (PIPE) {
+      load_k(list, min(U, total), kv);
+      for (int i = 0; i < total; i += U) {
+        const int nu = min(U, total - i);
+        load_v(list + i, nu, vv);
+        ha(nu, kv);
+        if (i + U < total) load_k(list + i + U, min(U, total - i - U), kv);
+        hb(nu, vv);
+      }
+    } else {
+      for (int i = 0; i < total; i += U) {
+        const int nu = min(U, total - i);
+        load_kv(list + i, nu, kv, vv);
+        ha(nu, kv);
+        hb(nu, vv);
+      }
+    }
+  };
 
   for (int s0 = 0; s0 <= t; s0 += kListCap) {
     // Lane l scans entries s0 + 8l .. s0 + 8l + 7 (two float4).
@@ -269,11 +325,8 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
     for (int c = 0; c < 8; ++c)
       if (keep[c]) list[p++] = sb + c;
     wave_lds_sync();
-    if (use_rs) {
-      for (int i = 0; i < total; i += U) process_rs(list + i, min(U, total - i));
-    } else {
-      for (int i = 0; i < total; i += U) process(list + i, min(U, total - i));
-    }
+    if (use_rs) run_groups(total, half_a_rs, half_b_rs);
+    else run_groups(total, half_a, half_b);
     wave_lds_sync();
   }
   if (use_rs) {

@@ -225,7 +225,7 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
                                                           reinterpret_cast<uint32_t*>(list),
                                                           rlo, rhi, rbad);
     // attention over keys with score >= thr.
-    attend_query<Tag, EK, EV>(
+    attend_query<Tag, EK, EV, true>(
         Q, K, V, t, a.HQ, a.DQ, a.DV, a.scale_log2, thr,
         [&](int s, float(&sv)[4]) {
           const float4 f = *reinterpret_cast<const float4*>(row + s);
