@@ -34,9 +34,11 @@
 //                   lane group g are keys {4g..4g+3} of key tile 2j and of
 //                   key tile 2j+1
 //                   -> lane l: query l%16, dims 4(l/16)+r of each 16-dim tile
-// P is rounded to the input's 16-bit type for the second product (the
-// reference multiplies fp32 probabilities; the difference is far inside the
-// 16-bit tolerance); everything else is fp32.  Rows that select nothing get
+// P is rounded to the input's 16-bit type for the second product and for
+// the softmax normaliser, which is one more MFMA per fragment (ones . P^T),
+// so numerator and denominator sum the same probabilities (the reference
+// uses fp32 probabilities; the difference is far inside the 16-bit
+// tolerance); everything else is fp32.  Rows that select nothing get
 // 0/0 = NaN, as the reference.
 #include "dsa_device.h"
 #include "dsa_launch.h"
@@ -72,6 +74,7 @@ struct Mfma16x16x32<BF16> {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
+  static constexpr uint32_t kOnes = 0x3f803f80u;  // two bf16 1.0
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) {  // one v_cvt_pk_bf16_f32
     typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
     typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -85,6 +88,7 @@ struct Mfma16x16x32<F16> {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
+  static constexpr uint32_t kOnes = 0x3c003c00u;  // two f16 1.0
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
     typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
     typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -201,7 +205,11 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
   }
 
   float m[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()};
-  float l[2] = {0.f, 0.f};
+  // Softmax normaliser per query as an MFMA accumulator: ones . P^T sums the
+  // tile's (16-bit) probabilities over all 64 keys of the tile, the same
+  // values the O product uses; every register of a query's lanes holds it.
+  f32x4 lacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  const u32x4 ones = u32x4{M::kOnes, M::kOnes, M::kOnes, M::kOnes};
   f32x4 o[NDT][2];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
@@ -315,16 +323,11 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
       m[qt] = m_new;
       const float m_use = (m_new == -__builtin_huge_valf()) ? 0.f : m_new;
       float p[4][4];
-      float ps = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          // bare v_exp_f32; exp2(-inf) = 0 for unselected keys
+        for (int r = 0; r < 4; ++r)  // bare v_exp_f32; exp2(-inf) = 0 for unselected keys
           p[j][r] = __builtin_amdgcn_exp2f(fmaf(st[j][qt][r], a.scale_log2, -m_use));
-          ps += p[j][r];
-        }
-      l[qt] = fmaf(l[qt], alpha[qt], ps);
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj)
         pf[qt][jj] = u32x4{M::pack(p[2 * jj][0], p[2 * jj][1]), M::pack(p[2 * jj][2], p[2 * jj][3]),
@@ -338,7 +341,15 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
         for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
           for (int r = 0; r < 4; ++r) o[dt][qt][r] *= alpha[qt];
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) lacc[qt][r] *= alpha[qt];
     }
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) lacc[qt] = M::run(ones, pf[qt][jj], lacc[qt]);
 
     // O^T += V^T . P^T.  Lane (g, j=c16) addresses V row key0 + 4g + j/4,
     // dims 16dt + 4(j%4) .. +3; rows key0 + 16 and + 32 keep the swizzle, so
@@ -387,9 +398,7 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
   // O = O^T / l, lane l: query tq[qt], dims 16dt + 4g .. +3.
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
-    float lt = l[qt];
-    lt = sum_xor32(sum_xor16(lt));
-    const float inv = 1.f / lt;  // lt == 0 only if nothing passed: NaN, as the reference
+    const float inv = 1.f / lacc[qt][0];  // lt == 0 only if nothing passed: NaN, as the reference
     if (tq[qt] < T) {
       float* orow = a.out + ((b * T + tq[qt]) * HQ + h) * static_cast<int64_t>(D);
 #pragma unroll
