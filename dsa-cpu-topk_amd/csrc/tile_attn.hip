@@ -263,16 +263,19 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
     const bool inner = (s0 + kKT - 1 <= tw) && (tw + 31 < T);  // every entry causal
     bool any = false;
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
+    for (int qt = 0; qt < 2; ++qt) {
+      // key s0 + 16j + 4g + r is causal for query tq iff 16j + r <= tq - s0 - 4g:
+      // one compare against a constant per entry
+      const int dq = (tq[qt] < T) ? tq[qt] - s0 - 4 * g : -1;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int s = s0 + 16 * j + 4 * g + r;
           // NaN scores and thresholds select nothing
-          sel[qt][j][r] = (inner | ((s <= tq[qt]) & (tq[qt] < T))) & (sv[qt][j][r] >= thr[qt]);
+          sel[qt][j][r] = (inner | (16 * j + r <= dq)) & (sv[qt][j][r] >= thr[qt]);
           any |= sel[qt][j][r];
         }
+    }
     return s0 <= wave_last && __ballot(any) != 0;
   };
 
