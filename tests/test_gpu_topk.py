@@ -65,6 +65,33 @@ def test_special_values(dev):
         check_rows(x, k, dev, what="special")
 
 
+@pytest.mark.parametrize("n", [300, 1000, 2048, 4096])
+def test_nan_inf_rows_threshold_only(dev, n):
+    """Threshold-only rows with non-finite values (rows up to 2048 entries
+    take one wave per row, 4096 the block kernel): NaN is the largest value
+    (torch.topk's order), +-inf and -0 as keys order them, and heavy ties
+    take the radix fallback; every k checked against torch.topk."""
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn((8, n), generator=g)
+    x[0, ::7] = float("nan")
+    x[1, ::5] = float("inf")
+    x[1, 1::5] = float("-inf")
+    x[2] = torch.where(torch.rand(n, generator=g) < 0.5, 1.0, float("nan"))
+    x[3] = torch.randint(0, 3, (n,), generator=g).float()        # three values, heavy ties
+    x[3, 17] = float("nan")
+    x[4] = float("-inf")
+    x[4, 3] = 0.0
+    x[5] = torch.where(torch.rand(n, generator=g) < 0.5, 0.0, -0.0)
+    x[6] = x[6] * 1e-42                                            # denormal magnitudes
+    x[7, :] = 3.0e38
+    x[7, ::3] = -3.0e38
+    xg = x.to(dev)
+    for k in sorted({1, 2, 7, n // 3, n // 2, n - 1, n}):
+        say(f"topk nan/inf n={n} k={k}")
+        torch.testing.assert_close(topk_threshold(xg, k).cpu(), O.topk_threshold(x, k),
+                                   rtol=0, atol=0, equal_nan=True, msg=f"n={n} k={k}")
+
+
 def test_bracket_path_misses_fall_back(dev):
     """Threshold-only rows above 4096 entries are selected in one pass from a
     bracket that an evenly spread 4096-entry sample (chunks 0, 4, 8, 12 of
