@@ -17,6 +17,9 @@ CONFIGS = {
     "c2_b16_k128": (16, 512, 128, 4, 32, 4, 32, 32, torch.float32),
     "c2_b32_k64": (32, 512, 64, 4, 32, 4, 32, 32, torch.float32),
     "c2_b64_k64": (64, 512, 64, 4, 32, 4, 32, 32, torch.float32),
+    # config-1 widths around the fused kernel's tile pairing (tests only)
+    "c1_t500": (16, 500, 32, 4, 32, 4, 32, 32, torch.float32),
+    "c1_t496": (16, 496, 32, 4, 32, 4, 32, 32, torch.float32),
     "c3": (4, 4096, 256, 8, 64, 8, 64, 64, torch.float32),
     "c4": (1, 16384, 2048, 64, 128, 16, 128, 128, torch.bfloat16),
 }

@@ -37,21 +37,22 @@ def test_fused_matches_oracle(dev, T, top_k, BLOCK_S):
     assert float((out.double() - ref).abs().max()) < 5e-4
 
 
-@pytest.mark.parametrize("T,top_k", [(256, 32), (512, 100)])
-def test_fused_tie_heavy_scores(dev, T, top_k):
+@pytest.mark.parametrize("B,T,top_k", [(2, 256, 32), (2, 512, 100), (16, 512, 32)])
+def test_fused_tie_heavy_scores(dev, B, T, top_k):
     """Integer-valued indexer inputs give exactly representable, heavily tied
     scores (the same in fp32 and float64), so the fused kernel's in-LDS
     select must keep exactly the oracle's tied set; batch element 1 has all
-    scores 0 (one value in every row)."""
+    scores 0 (one value in every row).  B=16, T=512 runs the config-1 grid
+    (long and short tiles paired per CU)."""
     g = torch.Generator().manual_seed(T)
-    B, HI, DI, HQ, DH = 2, 4, 32, 4, 32
+    HI, DI, HQ, DH = 4, 32, 4, 32
     qi = torch.randint(-1, 2, (B, T, HI, DI), generator=g).float()
     ki = torch.randint(-1, 2, (B, T, DI), generator=g).float()
     wi = torch.randint(1, 3, (B, T, HI), generator=g).float()
     qi[1] = 0.0
     Q, K, V = (torch.randn((B, T, HQ, DH), generator=g) for _ in range(3))
     ins = (qi, ki, wi, Q, K, V)
-    say(f"fused tie-heavy T={T} k={top_k}")
+    say(f"fused tie-heavy B={B} T={T} k={top_k}")
     out = D.dsa_fused_hip(*to_dev(ins, dev), top_k).cpu()
     ref = O.dsa_forward(*ins, top_k)
     assert float((out.double() - ref).abs().max()) < 5e-4
@@ -136,6 +137,14 @@ def staged_check(dev, name, rows=None, rtol=1e-4, atol=1e-4, max_flip_frac=0.005
 @pytest.mark.parametrize("name", ["c0", "c1", "c2_b4_k64", "c2_b16_k64", "c2_b16_k128",
                                   "c2_b32_k64", "c2_b64_k64"])
 def test_configs_t512(dev, name):
+    staged_check(dev, name)
+
+
+@pytest.mark.parametrize("name", ["c1_t500", "c1_t496"])
+def test_fused_tile_pairing_edges(dev, name):
+    """Config-1 widths around the fused kernel's tile pairing per CU: T=500
+    has a partial last tile (rows past T in the longest tile), T=496 an odd
+    tile count."""
     staged_check(dev, name)
 
 
