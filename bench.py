@@ -507,7 +507,9 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build has no "
-              "multi-GPU path; see DESIGN.md for how the forward would shard.", file=sys.stderr)
+              "multi-GPU path (the forward would shard by batch element, one process per "
+              "GPU, or by zig-zag query tiles after one all-gather of k_idx, K and V).",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
