@@ -20,6 +20,8 @@ CONFIGS = {
     # config-1 widths around the fused kernel's tile pairing (tests only)
     "c1_t500": (16, 500, 32, 4, 32, 4, 32, 32, torch.float32),
     "c1_t496": (16, 496, 32, 4, 32, 4, 32, 32, torch.float32),
+    # the fused kernel's largest T (16-query blocks: the most LDS it takes)
+    "fused_t2048": (2, 2048, 64, 4, 32, 4, 32, 32, torch.float32),
     "c3": (4, 4096, 256, 8, 64, 8, 64, 64, torch.float32),
     "c4": (1, 16384, 2048, 64, 128, 16, 128, 128, torch.bfloat16),
 }

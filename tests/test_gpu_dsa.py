@@ -148,6 +148,12 @@ def test_fused_tile_pairing_edges(dev, name):
     staged_check(dev, name)
 
 
+def test_fused_at_max_T(dev):
+    """T = 2048, the fused kernel's limit (dsa_fused_max_T), with 16-query
+    blocks whose score rows take the most LDS; fused and split must agree."""
+    staged_check(dev, "fused_t2048", rows=sample_rows(2048, 16, include=(0, 63, 64, 1023, 2047)))
+
+
 def test_config3(dev):
     staged_check(dev, "c3", rows=sample_rows(4096, 24, include=(0, 254, 255, 256, 4095)))
 
