@@ -311,6 +311,101 @@ def bench_stream(dev, cfg, dtype, name, nbatch=4, reps=3):
     return res
 
 
+def time_reference_style(fn, stream, warmup=5, iters=20):
+    """The reference's timing (bench_hybrid.py:26-37): warm-up calls, then
+    HIP events on the stream around `iters` Python calls; ms per call.  Host
+    work inside fn (launch path, host waits) is inside the figure."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(iters):
+        fn()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters
+
+
+def bench_hybrid(dev):
+    """The reference's experiment (bench_hybrid.py:40-53, dsa_hybrid.py:46-66)
+    on this box: the whole CPU-offload forward -- GPU indexer, pinned d2h, host
+    k-th largest (libdsa_cpu.so), h2d, GPU attention -- against the all-GPU
+    fused and split forwards, each timed the reference's way (events around
+    Python calls).  `hybrid` is the reference's pipeline step for step;
+    `hybrid_pipelined` copies in 4 row blocks and selects each block as it
+    lands, reading only the causal half of each row."""
+    import torch
+
+    import dsa_attention as D
+    from dsa_hybrid import HybridContext, dsa_hybrid_cpu_topk, dsa_hybrid_stream
+
+    stream = torch.cuda.current_stream(dev)
+    rows = []
+    for B, k in [(C1["B"], C1["k"])] + [(b, kk) for b, kk, _ in C2_SWEEP]:
+        cfg = dict(C1, B=B, k=k)
+        ins = gpu_inputs(cfg, torch.float32, dev, seed=B + k)
+        ctx = HybridContext(B, cfg["T"], device=dev)
+        hyb = dsa_hybrid_cpu_topk(*ins, k, ctx=ctx)
+        equal = bool(torch.equal(hyb, D.dsa_split_hip(*ins, k)))
+        legs = {
+            "fused_ms": lambda: D.dsa_attention_triton(*ins, top_k=k),
+            "split_ms": lambda: D.dsa_attention_split_triton(*ins, top_k=k),
+            "hybrid_ms": lambda: dsa_hybrid_cpu_topk(*ins, k, ctx=ctx),
+            "hybrid_pipelined_ms": lambda: dsa_hybrid_cpu_topk(*ins, k, ctx=ctx, chunks=4,
+                                                               causal=True),
+        }
+        row = {"B": B, "T": cfg["T"], "k": k, "hybrid_equals_split": equal}
+        for name, fn in legs.items():
+            row[name] = round(time_reference_style(fn, stream), 4)
+        rows.append(row)
+        del ins, ctx, hyb
+    # batch streaming of the hybrid path: config 2 (B=4, k=64) x 16 batches
+    nb = 16
+    batches = [gpu_inputs(C2, torch.float32, dev, seed=40 + i) for i in range(nb)]
+    ctx = HybridContext(C2["B"], C2["T"], device=dev)
+
+    def one_by_one():
+        for bt in batches:
+            dsa_hybrid_cpu_topk(*bt, C2["k"], ctx=ctx, causal=True)
+        torch.cuda.synchronize()
+
+    streamed = lambda: dsa_hybrid_stream(batches, C2["k"], causal=True)  # noqa: E731
+    res = {"workload": "CPU-offload DSA forward (host k-th largest) vs all-GPU, config 1 and "
+                       "the config-2 sweep (T=512, fp32); ms per forward, events around "
+                       "Python calls as bench_hybrid.py times them",
+           "host_isa": "avx512" if __import__("_dsa_lib").cpu_lib().dsa_cpu_isa() else "scalar",
+           "host_threads": int(os.environ.get("OMP_NUM_THREADS", "0")) or
+           len(os.sched_getaffinity(0)),
+           "rows": rows}
+    t_seq = time_reference_style(one_by_one, stream, warmup=1, iters=3)
+    t_str = time_reference_style(streamed, stream, warmup=1, iters=3)
+    res["stream_c2x16"] = {"one_by_one_ms": round(t_seq, 3), "streamed_ms": round(t_str, 3),
+                           "note": "host select of batch i during the GPU indexer + d2h of "
+                                   "batch i+1 (dsa_hybrid_stream)"}
+    return res
+
+
+def bench_eager_latency(dev):
+    """Per-call latency of the drop-ins at config 1 as the reference measures
+    its own (bench_hybrid.py:26-37: 5 warm-up calls, events around 20 Python
+    calls), launch path included."""
+    import torch
+
+    import dsa_attention as D
+
+    ins = gpu_inputs(C1, torch.float32, dev)
+    stream = torch.cuda.current_stream(dev)
+    k = C1["k"]
+    return {"dsa_attention_triton_ms": round(time_reference_style(
+                lambda: D.dsa_attention_triton(*ins, top_k=k), stream), 4),
+            "dsa_attention_split_triton_ms": round(time_reference_style(
+                lambda: D.dsa_attention_split_triton(*ins, top_k=k), stream), 4),
+            "method": "5 warm-up calls, HIP events around 20 Python calls (bench_hybrid.py:26-37)"}
+
+
 def bench_projection(dev, reps=20):
     """Projection front end (informational): three projection GEMMs + the
     indexer (the reference's indexer_triton structure) against one fused
@@ -426,6 +521,7 @@ def cpu_baseline(dev=None, budget_s=12.0):
     res["topk_avx512"] = {"kind": kind, "ms": round(topk_ms, 4),
                           "sample": "config-1 scores [16,512,512], k=32", "cores": cores,
                           "avx512": "avx512f" in native.cpu_flags()}
+    res.update(cpu_baseline_wide(cores))
     if dev is not None:
         # The reference's hybrid path (dsa_hybrid.py:46-66) on this host: the
         # score matrix crosses PCIe to pinned memory, the CPU selects, the
@@ -445,6 +541,83 @@ def cpu_baseline(dev=None, budget_s=12.0):
             "h2d_ms": round(h2d * 1e3, 4),
             "offload_ms": round(d2h * 1e3 + topk_ms + h2d * 1e3, 4)}
     return res
+
+
+def _evenly(T, n):
+    """n query rows spread evenly over 0..T-1 (the causal cost of a row grows
+    with t, so their mean cost is the mean cost of all T rows)."""
+    return [int((i + 0.5) * T / n) for i in range(n)]
+
+
+def cpu_baseline_wide(cores, budget_s=4.0):
+    """The reference's CPU path beyond config 1 (bounded samples, each named):
+      * the AVX-512 k-th largest on the standalone [64,2048,2048] k=128 rows
+        (the reference publishes 143.9 ms there, README.md:67; method
+        bench_avx512.py:25-52): the reference's own source (oracle/_ref) and
+        this repo's host library (libdsa_cpu.so, the CPU-offload select);
+      * the torch-vectorised fp32 forward (oracle restatement of
+        dsa_attention_torch) at configs 3 and 4 on evenly spread query rows,
+        chunked over rows, scaled to a whole forward;
+      * the k-th largest on config-4 score rows (real indexer scores, -inf
+        past the diagonal) for the same sampled rows."""
+    import torch
+
+    from oracle import dsa_oracle as O
+    from oracle import native
+    from topk_threshold import topk_threshold
+
+    out = {}
+    ref = native.ref()
+
+    def timed(fn, min_reps=3):
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while n < min_reps or time.perf_counter() - t0 < budget_s / 4:
+            fn()
+            n += 1
+        return (time.perf_counter() - t0) / n * 1e3
+
+    x = torch.randn((64, 2048, 2048), generator=torch.Generator().manual_seed(0))
+    row = {"workload": "[64,2048,2048] N(0,1) fp32, k=128 (config 2 standalone)",
+           "cores": cores, "reference_published_ms": 143.9,
+           "reference_published_on": "Ryzen 9 9950X3D, 16 threads (README.md:67)",
+           "host_lib_ms": round(timed(lambda: topk_threshold(x, 128)), 3)}
+    if ref is not None:
+        row["reference_build_ms"] = round(timed(lambda: ref.topk_threshold(x, 128)), 3)
+        row["equal"] = bool(torch.equal(ref.topk_threshold(x, 128), topk_threshold(x, 128)))
+    out["topk_c2_standalone"] = row
+    del x
+
+    for name, cfg, dt, nrows in (("c3", C3, torch.float32, 256), ("c4", C4, torch.bfloat16, 128)):
+        B, T, k = cfg["B"], cfg["T"], cfg["k"]
+        ins = O.make_inputs(B, T, cfg["HI"], cfg["DI"], cfg["HQ"], cfg["DQ"], cfg["DV"],
+                            dtype=dt, w_scale=(1 / 8 if name == "c4" else None))
+        rows = _evenly(T, nrows)
+        chunk = O._chunk_rows(len(rows), B * max(cfg["HI"], cfg["HQ"]) * T)
+        t0 = time.perf_counter()
+        _, sc, _ = O.dsa_forward(*ins, k, acc=torch.float32, rows=rows, return_parts=True)
+        dt_s = time.perf_counter() - t0
+        est_ms = dt_s * (T / nrows) * 1e3
+        out[f"forward_{name}"] = {
+            "workload": f"config {name[1]}: torch-vectorised fp32 forward (oracle restatement of "
+                        f"dsa_attention_torch; {str(dt).replace('torch.', '')} inputs upcast)",
+            "sample": f"{B}x{nrows} query rows spread evenly over T={T} (t = (i+0.5)*T/{nrows}), "
+                      f"{chunk} rows per chunk; {dt_s:.2f} s, scaled by T/{nrows}",
+            "est_ms_per_forward": round(est_ms, 1),
+            "query_tokens_per_s": round(B * T / (est_ms / 1e3), 1), "cores": cores}
+        if name == "c4":
+            scf = sc.float().contiguous()              # [1, nrows, T], -inf past each t
+            r4 = {"workload": f"k-th largest (k={k}) of {nrows} config-4 score rows "
+                              f"[1,{nrows},{T}] (real indexer scores, full rows)",
+                  "host_lib_ms": round(timed(lambda: topk_threshold(scf, k)), 4)}
+            if ref is not None:
+                r4["reference_build_ms"] = round(timed(lambda: ref.topk_threshold(scf, k)), 4)
+                r4["equal"] = bool(torch.equal(ref.topk_threshold(scf, k),
+                                               topk_threshold(scf, k)))
+            r4["host_lib_est_ms_all_rows"] = round(r4["host_lib_ms"] * T / nrows, 2)
+            out["topk_c4_rows"] = r4
+        del ins, sc
+    return out
 
 
 def pmc_workload(args, dev):
@@ -497,6 +670,7 @@ def main():
     ap.add_argument("--mode", choices=("graph", "eager"), default="graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-select", action="store_true", help="skip the config-4 select leg")
+    ap.add_argument("--no-hybrid", action="store_true", help="skip the CPU-offload legs")
     ap.add_argument("--no-long", action="store_true",
                     help="skip the split-forward legs at configs 3 and 4")
     ap.add_argument("--pmc-workload", action="store_true",
@@ -574,6 +748,11 @@ def main():
             "c3": bench_stream(dev, C3, torch.float32, "config 3"),
             "c4": bench_stream(dev, C4, torch.bfloat16, "config 4"),
         }
+    log("bench: eager per-call latency at config 1")
+    out["eager_latency_c1"] = bench_eager_latency(dev)
+    if not args.no_hybrid:
+        log("bench: CPU-offload (hybrid) forward")
+        out["hybrid"] = bench_hybrid(dev)
     if not args.no_cpu:
         log("bench: CPU baseline")
         out["cpu_baseline"] = cpu_baseline(dev)

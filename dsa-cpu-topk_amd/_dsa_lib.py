@@ -1,4 +1,6 @@
-"""ctypes binding of libdsa_amd.so (the C ABI declared in include/dsa_amd.h).
+"""ctypes bindings of libdsa_amd.so (the gfx950 kernels, include/dsa_amd.h)
+and libdsa_cpu.so (the host k-th largest of the CPU-offload path,
+include/dsa_cpu.h).
 
 The library is loaded after torch so that it binds to the HIP runtime torch
 already loaded (one runtime per process: streams and device pointers are
@@ -18,11 +20,13 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libdsa_amd.so")
+CPU_LIB_PATH = os.path.join(HERE, "libdsa_cpu.so")
 
 DSA_F32, DSA_BF16, DSA_F16, DSA_FP8 = 0, 1, 2, 3
 DSA_OK, DSA_EINVAL, DSA_EUNSUPPORTED, DSA_EHIP = 0, -1, -2, 1
 
 _lib = None
+_cpu_lib = None
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -46,6 +50,13 @@ _SIGNATURES = {
 }
 
 
+_CPU_SIGNATURES = {
+    "dsa_cpu_last_error": ([], ctypes.c_char_p),
+    "dsa_cpu_isa": ([], _I),
+    "dsa_cpu_topk_threshold": ([_P, _I64, _I64, _I64, _I, _I64, _I64, _P, _I], _I),
+}
+
+
 class DSAUnsupported(AssertionError):
     """A shape the library has no kernel instance for (status DSA_EUNSUPPORTED)."""
 
@@ -65,6 +76,23 @@ def lib():
             fn.restype = res
         _lib = handle
     return _lib
+
+
+def cpu_lib():
+    """The loaded host library (raises RuntimeError if it was never built)."""
+    global _cpu_lib
+    if _cpu_lib is None:
+        if not os.path.exists(CPU_LIB_PATH):
+            raise RuntimeError(
+                f"{CPU_LIB_PATH} is not built; run `python dsa-cpu-topk_amd/build_native.py` "
+                "(or __graft_entry__.build()).")
+        handle = ctypes.CDLL(CPU_LIB_PATH)
+        for name, (args, res) in _CPU_SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = res
+        _cpu_lib = handle
+    return _cpu_lib
 
 
 def check(rc: int, what: str) -> None:

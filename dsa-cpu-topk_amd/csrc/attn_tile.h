@@ -27,12 +27,15 @@ namespace dsa {
 constexpr int kListCap = 512;  // one 512-entry segment of the score row
 
 // This lane's slice of query row t, times scale_log2 (0 past the row).
+// EQ: elements the wave covers (its heads times DQ); RQ: elements from one
+// query row to the next (EQ, or HQ*DQ when the wave covers a head chunk).
 template <typename Tag, int EK>
 __device__ __forceinline__ void load_query(const typename Tag::raw* __restrict__ Q, int t,
-                                           int EQ, float scale_log2, float (&q)[EK]) {
+                                           int EQ, float scale_log2, float (&q)[EK],
+                                           int RQ = 0) {
   const int lane = lane_id();
   if (lane * EK < EQ) {
-    load_cvt<Tag, EK>(Q + static_cast<int64_t>(t) * EQ + lane * EK, q);
+    load_cvt<Tag, EK>(Q + static_cast<int64_t>(t) * (RQ > 0 ? RQ : EQ) + lane * EK, q);
 #pragma unroll
     for (int e = 0; e < EK; ++e) q[e] *= scale_log2;
   } else {
@@ -47,6 +50,10 @@ __device__ __forceinline__ void load_query(const typename Tag::raw* __restrict__
 // (nullptr: loaded here).  PIPE: overlap each group's loads with the
 // neighbouring group's arithmetic (below); it needs more registers, which
 // the fused kernel has to spare and the gather kernel's occupancy does not.
+// Head chunks: HQ may be a subset of a row's heads (rows too wide for one
+// wave's registers).  Then Q/K/V/out_row point at the chunk's first head
+// and RQ / RV give the full row lengths (elements of a Q or K row, of a V
+// row); 0 means the row is exactly the HQ heads.
 template <typename Tag, int EK, int EV, bool PIPE = false, typename Load4>
 __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict__ Q,
                                              const typename Tag::raw* __restrict__ K,
@@ -54,11 +61,14 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
                                              int HQ, int DQ, int DV, float scale_log2,
                                              float thr, Load4&& load4, int* list,
                                              float* __restrict__ out_row,
-                                             const float* qpre = nullptr) {
+                                             const float* qpre = nullptr, int RQ = 0,
+                                             int RV = 0) {
   using raw = typename Tag::raw;
   const int lane = lane_id();
   const int EQ = HQ * DQ;
   const int EVt = HQ * DV;
+  const int rowq = RQ > 0 ? RQ : EQ;   // elements per Q / K row
+  const int rowv = RV > 0 ? RV : EVt;  // elements per V row
   const bool kact = lane * EK < EQ;
   const bool vact = lane * EV < EVt;
   const int lphk = DQ / EK;                     // lanes per head, K side
@@ -71,7 +81,7 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
 #pragma unroll
     for (int e = 0; e < EK; ++e) q[e] = qpre[e];
   } else {
-    load_query<Tag, EK>(Q, t, EQ, scale_log2, q);
+    load_query<Tag, EK>(Q, t, EQ, scale_log2, q, rowq);
   }
   float acc[EV];
 #pragma unroll
@@ -115,7 +125,7 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
 #pragma unroll
     for (int u = 0; u < U; ++u)
       load_cvt<Tag, EK>(reinterpret_cast<const raw*>(
-                            Kb + (sidx[u] * (static_cast<uint32_t>(EQ) * kRaw) + koff_l)),
+                            Kb + (sidx[u] * (static_cast<uint32_t>(rowq) * kRaw) + koff_l)),
                         kv[u]);
   };
   auto load_v = [&](const int* ss, int nu, float (&vv)[U][EV]) {
@@ -124,7 +134,7 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
 #pragma unroll
     for (int u = 0; u < U; ++u)
       load_cvt<Tag, EV>(reinterpret_cast<const raw*>(
-                            Vb + (sidx[u] * (static_cast<uint32_t>(EVt) * kRaw) + voff_l)),
+                            Vb + (sidx[u] * (static_cast<uint32_t>(rowv) * kRaw) + voff_l)),
                         vv[u]);
   };
   auto load_kv = [&](const int* ss, int nu, float (&kv)[U][EK], float (&vv)[U][EV]) {
@@ -132,8 +142,8 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
     group_keys(ss, nu, sidx);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint32_t rk = sidx[u] * (static_cast<uint32_t>(EQ) * kRaw);
-      const uint32_t rv = (EQ == EVt) ? rk : sidx[u] * (static_cast<uint32_t>(EVt) * kRaw);
+      const uint32_t rk = sidx[u] * (static_cast<uint32_t>(rowq) * kRaw);
+      const uint32_t rv = (rowq == rowv) ? rk : sidx[u] * (static_cast<uint32_t>(rowv) * kRaw);
       load_cvt<Tag, EK>(reinterpret_cast<const raw*>(Kb + (rk + koff_l)), kv[u]);
       load_cvt<Tag, EV>(reinterpret_cast<const raw*>(Vb + (rv + voff_l)), vv[u]);
     }

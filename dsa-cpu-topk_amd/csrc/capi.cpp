@@ -70,6 +70,8 @@ int check_attn(int dtype, int64_t B, int64_t T, int HQ, int DQ, int DV, const vo
   if (T * HQ * static_cast<int64_t>(DQ > DV ? DQ : DV) * esize > (int64_t{1} << 32) - 1)
     return fail(DSA_EINVAL, "%s: T*HQ*max(DQ,DV) = %lld elements of %lld bytes must be < 4 GiB", who,
                 (long long)(T * HQ * static_cast<int64_t>(DQ > DV ? DQ : DV)), (long long)esize);
+  if (B * ((T + 3) / 4) * static_cast<int64_t>(HQ) > (int64_t{1} << 32) - 1)
+    return fail(DSA_EINVAL, "%s: B*T*HQ too large for one launch", who);
   if (B * T == 0) return DSA_OK;
   if (!Q || !K || !V || !out) return fail(DSA_EINVAL, "%s: null pointer", who);
   if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(out))
@@ -164,6 +166,10 @@ int dsa_sparse_attn_threshold_tiled(const float* scores, int64_t ld, const float
   if (!std::isfinite(scale)) return fail(DSA_EINVAL, "sparse_attn_tiled: scale must be finite");
   if (dtype == DSA_F32 || DQ != DV || (DQ != 64 && DQ != 128))
     return fail(DSA_EUNSUPPORTED, "sparse_attn_tiled: needs bf16/fp16 and DQ = DV in {64,128} (dtype %d DQ=%d DV=%d)", dtype, DQ, DV);
+  // the tile DMA addresses one batch element's K/V rows with 32-bit byte offsets
+  if (T * HQ * static_cast<int64_t>(DQ) * 2 > (int64_t{1} << 32) - 1)
+    return fail(DSA_EINVAL, "sparse_attn_tiled: T*HQ*D = %lld 16-bit elements must be < 4 GiB",
+                (long long)(T * HQ * static_cast<int64_t>(DQ)));
   if (B * T == 0) return DSA_OK;
   if (!scores || !thr || !Q || !K || !V || !out) return fail(DSA_EINVAL, "sparse_attn_tiled: null pointer");
   if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(out))

@@ -27,6 +27,13 @@ hipError_t launch_sparse_attn(const float* scores, int64_t ld, const float* thr,
                               int HQ, int DQ, int DV, float scale, float* out,
                               hipStream_t stream);
 bool sparse_attn_supported(int dtype, int HQ, int DQ, int DV);
+// The per-query gather kernel alone (launch_sparse_attn may pick tiles), and
+// whether it splits a row into head chunks for this shape.
+hipError_t launch_sparse_attn_gather(const float* scores, int64_t ld, const float* thr,
+                                     const void* Q, const void* K, const void* V, int dtype,
+                                     int64_t B, int64_t T, int HQ, int DQ, int DV, float scale,
+                                     float* out, hipStream_t stream);
+bool sparse_attn_chunked(int dtype, int HQ, int DQ, int DV);
 
 // The same attention as dense-masked MFMA tiles (tile_attn.hip).  The
 // threshold entry point switches to it at T >= kTiledMinT when it applies.

@@ -8,6 +8,10 @@
 //
 // Block = 4 waves = 4 consecutive queries of one batch element.  Blocks run
 // longest query first, spread evenly over the XCDs (causal_block_tile).
+// Rows wider than one wave's registers hold (more than 16 fp32 or 32 16-bit
+// elements per lane) are split into head chunks: each block then takes one
+// chunk of its 4 queries' heads, and the chunks of a tile are adjacent
+// blocks (they read the same score rows, one after another, from L2).
 //
 // For long rows (T >= kTiledMinT) with 16-bit inputs and DQ = DV in {64,
 // 128}, launch_sparse_attn hands over to the dense-masked MFMA tile kernel
@@ -32,6 +36,8 @@ struct AttnArgs {
   float scale_log2;
   float* out;
   int vec;
+  int HQc;     // heads per chunk
+  int nchunk;  // HQ / HQc
 };
 
 template <typename Tag, int EK, int EV>
@@ -41,22 +47,25 @@ __global__ __launch_bounds__(256) void sparse_attn_kernel(AttnArgs a) {
   const int wave = threadIdx.x >> 6;
   const int T = a.T;
   const int tiles = (T + 3) >> 2;
+  const int chunk = static_cast<int>(blockIdx.x % static_cast<uint32_t>(a.nchunk));
   int64_t b;
   int tile;
-  causal_block_tile(blockIdx.x, a.B, tiles, b, tile);
+  causal_block_tile(blockIdx.x / static_cast<uint32_t>(a.nchunk), a.B, tiles, b, tile);
   const int t = tile * 4 + wave;
   if (t >= T) return;
   const int64_t EQ = static_cast<int64_t>(a.HQ) * a.DQ;
   const int64_t EVt = static_cast<int64_t>(a.HQ) * a.DV;
-  const raw* Q = static_cast<const raw*>(a.Q) + b * T * EQ;
-  const raw* K = static_cast<const raw*>(a.K) + b * T * EQ;
-  const raw* V = static_cast<const raw*>(a.V) + b * T * EVt;
+  const int64_t cq = static_cast<int64_t>(chunk) * a.HQc * a.DQ;  // chunk's first element
+  const int64_t cv = static_cast<int64_t>(chunk) * a.HQc * a.DV;
+  const raw* Q = static_cast<const raw*>(a.Q) + b * T * EQ + cq;
+  const raw* K = static_cast<const raw*>(a.K) + b * T * EQ + cq;
+  const raw* V = static_cast<const raw*>(a.V) + b * T * EVt + cv;
   const int64_t qrow = b * T + t;
   const float* srow = a.scores + qrow * a.ld;
   const float thr = a.thr[qrow];
   const bool vec = a.vec != 0;
   attend_query<Tag, EK, EV>(
-      Q, K, V, t, a.HQ, a.DQ, a.DV, a.scale_log2, thr,
+      Q, K, V, t, a.HQc, a.DQ, a.DV, a.scale_log2, thr,
       [&](int s, float(&sv)[4]) {
         if (vec) {
           const float4 f = *reinterpret_cast<const float4*>(srow + s);
@@ -66,12 +75,13 @@ __global__ __launch_bounds__(256) void sparse_attn_kernel(AttnArgs a) {
           for (int c = 0; c < 4; ++c) sv[c] = (s + c <= t) ? srow[s + c] : 0.f;
         }
       },
-      lists[wave], a.out + qrow * EVt);
+      lists[wave], a.out + qrow * EVt + cv, nullptr, static_cast<int>(EQ),
+      static_cast<int>(EVt));
 }
 
 template <typename Tag, int EK, int EV>
 hipError_t launch(const AttnArgs& a, hipStream_t stream) {
-  const int64_t nblk = a.B * ((a.T + 3) / 4);
+  const int64_t nblk = a.B * ((a.T + 3) / 4) * a.nchunk;
   hipLaunchKernelGGL((sparse_attn_kernel<Tag, EK, EV>), dim3(static_cast<unsigned>(nblk)),
                      dim3(256), 0, stream, a);
   return hipGetLastError();
@@ -96,11 +106,30 @@ int elems_per_lane(int HQ, int D) {
 
 bool pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
+// Largest slice a lane holds: 16 fp32 or 32 16-bit elements (64 bytes).
+int max_elems(int dtype) { return dtype == 0 ? 16 : 32; }
+
+// Head chunks a row is split into so that a chunk's K and V rows fit one
+// wave at <= max_elems per lane (1 when the whole row fits).
+int head_chunks(int dtype, int HQ, int DQ, int DV) {
+  const int64_t width = static_cast<int64_t>(HQ) * (DQ > DV ? DQ : DV);
+  const int64_t cap = static_cast<int64_t>(kWave) * max_elems(dtype);
+  int n = 1;
+  while (width / n > cap && n < HQ) n *= 2;
+  return n;
+}
+
 }  // namespace
+
+bool sparse_attn_chunked(int dtype, int HQ, int DQ, int DV) {
+  return head_chunks(dtype, HQ, DQ, DV) > 1;
+}
 
 bool sparse_attn_supported(int dtype, int HQ, int DQ, int DV) {
   if (!pow2(HQ) || !pow2(DQ) || !pow2(DV)) return false;
-  const int EK = elems_per_lane(HQ, DQ), EV = elems_per_lane(HQ, DV);
+  const int HQc = HQ / head_chunks(dtype, HQ, DQ, DV);
+  const int EK = elems_per_lane(HQc, DQ), EV = elems_per_lane(HQc, DV);
+  if (EK > max_elems(dtype) || EV > max_elems(dtype)) return false;
   if (EK > DQ || EV > DV) return false;  // a lane's slice must stay inside one head
   if (dtype == 0) {
     DSA_ATTN_PAIRS(DSA_ATTN_HAS, F32)
@@ -115,12 +144,26 @@ hipError_t launch_sparse_attn(const float* scores, int64_t ld, const float* thr,
                               int HQ, int DQ, int DV, float scale, float* out,
                               hipStream_t stream) {
   if (B == 0 || T == 0) return hipSuccess;
-  if (T >= kTiledMinT && tile_attn_supported(dtype, HQ, DQ, DV, Q, K, V))
+  const int nchunk = head_chunks(dtype, HQ, DQ, DV);
+  // Dense-masked tiles for long rows, and for rows whose gathers would need
+  // head chunks (each chunk re-reads the score row and the list).
+  if ((T >= kTiledMinT || nchunk > 1) && tile_attn_supported(dtype, HQ, DQ, DV, Q, K, V))
     return launch_tile_attn(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, scale, out, stream);
+  return launch_sparse_attn_gather(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, DV, scale,
+                                   out, stream);
+}
+
+hipError_t launch_sparse_attn_gather(const float* scores, int64_t ld, const float* thr,
+                                     const void* Q, const void* K, const void* V, int dtype,
+                                     int64_t B, int64_t T, int HQ, int DQ, int DV, float scale,
+                                     float* out, hipStream_t stream) {
+  if (B == 0 || T == 0) return hipSuccess;
+  const int nchunk = head_chunks(dtype, HQ, DQ, DV);
+  const int HQc = HQ / nchunk;
   const bool vec = (ld % 4 == 0) && ((reinterpret_cast<uintptr_t>(scores) & 15u) == 0);
   AttnArgs a{scores, ld, thr, Q, K, V, B, static_cast<int>(T), HQ, DQ, DV,
-             scale * 1.4426950408889634f, out, vec ? 1 : 0};
-  const int EK = elems_per_lane(HQ, DQ), EV = elems_per_lane(HQ, DV);
+             scale * 1.4426950408889634f, out, vec ? 1 : 0, HQc, nchunk};
+  const int EK = elems_per_lane(HQc, DQ), EV = elems_per_lane(HQc, DV);
   if (dtype == 0) {
     DSA_ATTN_PAIRS(DSA_ATTN_CASE, F32)
   } else if (dtype == 1) {

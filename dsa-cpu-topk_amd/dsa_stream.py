@@ -1,13 +1,22 @@
-"""Batch streaming: the split DSA forward over a sequence of batches with the
-indexer of one batch overlapping the select and attention of the previous.
+"""Batch streaming: the split DSA forward over a sequence of batches.
 
 The reference sketches this for its hybrid path (DEVLOG.md:207-210: overlap
 the CPU top-K of batch i with the GPU indexer of batch i+1; "only matters in
-batch-streaming inference").  Here the whole forward is on the GPU, so the
-overlap is between GPU kernels with different limits: the indexer is
-MFMA-bound, the select HBM-bound and the attention issue/latency-bound.
+batch-streaming inference").  That overlap, with the host select, is
+dsa_hybrid.dsa_hybrid_stream.  With the whole forward on the GPU there is no
+host stage to hide, and each kernel fills the MI355X by itself, so:
 
-Two HIP streams (default priority) and `depth` score/threshold slots:
+  * dsa_attention_stream (the default form) runs the batches one after
+    another on the caller's stream with one reused score/threshold buffer;
+  * DSAStreamGraph captures N batches into one HIP graph (no per-launch host
+    cost: the form for serving loops of small batches);
+  * DSAStreamPipeline overlaps batch i+1's indexer with batch i's select and
+    attention on two streams.  Measured on MI355X it is slower than running
+    the batches one after another (config 2: ~3x, from its per-batch host
+    work; configs 3-4: no gain), so nothing here uses it by default.
+
+DSAStreamPipeline: two HIP streams (default priority) and `depth`
+score/threshold slots:
   indexer stream:    indexer(i) -> scores[i % depth]; event ready[i]
   attention stream:  wait ready[i]; select(i) -> thr[i % depth];
                      attention(i) -> out[i]; event done[i]
@@ -149,16 +158,40 @@ class DSAStreamGraph:
         self.graph.replay()
 
 
-def dsa_attention_stream(batches, top_k: int, depth: int = 2):
+def dsa_attention_stream(batches, top_k: int, depth: int | None = None):
     """Split forward over an iterable of (q_idx, k_idx, w_idx, Q, K, V)
-    batches of one shape, overlapped as DSAStreamPipeline describes; returns
-    the list of outputs (synchronised)."""
-    outs, pipe = [], None
+    batches of one shape; returns the list of outputs (synchronised).
+
+    Default: the batches one after another on the caller's stream, the score
+    and threshold buffers allocated once and reused.  depth=N runs them on
+    the two-stream DSAStreamPipeline with N slots instead (same outputs, bit
+    for bit; slower on MI355X as measured, kept for experiments)."""
+    outs = []
+    if depth is not None:
+        pipe = None
+        for bt in batches:
+            if pipe is None:
+                pipe = DSAStreamPipeline(bt[3].shape[0], bt[3].shape[1], top_k,
+                                         device=bt[3].device, depth=depth)
+            outs.append(pipe.submit(*bt))
+        if pipe is not None:
+            pipe.synchronize()
+        return outs
+    scores = thr = None
+    dev = None
     for bt in batches:
-        if pipe is None:
-            pipe = DSAStreamPipeline(bt[3].shape[0], bt[3].shape[1], top_k,
-                                     device=bt[3].device, depth=depth)
-        outs.append(pipe.submit(*bt))
-    if pipe is not None:
-        pipe.synchronize()
+        q_idx, k_idx, w_idx, Q, K, V = bt
+        L.require_gpu(q_idx, k_idx, w_idx, Q, K, V)
+        B, T = Q.shape[0], Q.shape[1]
+        if scores is None:
+            dev = Q.device
+            scores = torch.empty(B, T, T, device=dev)
+            thr = torch.empty(B, T, 1, device=dev)
+            k = min(top_k, T)
+        assert scores.shape == (B, T, T), "dsa_attention_stream: batches must share one shape"
+        indexer_scores_hip(q_idx, k_idx, w_idx, write_upper=False, out=scores)
+        topk_threshold_into(scores, k, thr, causal=True)
+        outs.append(sparse_attention_hip(scores, thr, Q, K, V))
+    if dev is not None:
+        torch.cuda.synchronize(dev)
     return outs

@@ -12,6 +12,9 @@ libdsa_amd.so (no Triton).  `indexer_scores_torch`, `project`,
 """
 from __future__ import annotations
 
+import weakref
+from collections import OrderedDict
+
 import torch
 
 import _dsa_lib as L
@@ -97,42 +100,112 @@ def indexer_scores_triton(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor,
     return indexer_scores_hip(q, k, w, write_upper=True)
 
 
-_WCAT_CACHE: dict = {}
+class _ProjectionWeightCache:
+    """Concatenated projection weights [W_Q | W_K | W_W | 0-pad], one entry
+    per set of weight tensors.
+
+    An entry is keyed on the identity of the three tensor objects and is
+    valid only while all three are alive (weak references), still hold the
+    same storage (data_ptr, shape, strides) and have not been modified in
+    place (`_version`).  A freed tensor's address can be handed to a new
+    tensor, so an address alone never identifies a weight: a new tensor is a
+    miss even when it lands where an old one lived.  An entry is dropped as
+    soon as one of its weights is garbage collected; at most `capacity`
+    entries (least recently used first out) are kept, e.g. one per layer.
+    """
+
+    def __init__(self, capacity: int = 64):
+        self.capacity = capacity
+        self._entries: "OrderedDict[tuple, tuple]" = OrderedDict()
+
+    @staticmethod
+    def _state(W: torch.Tensor) -> tuple:
+        return (W.data_ptr(), W._version, tuple(W.shape), W.stride(), W.dtype, W.device)
+
+    def get(self, W_Q, W_K, W_W, dtype) -> torch.Tensor:
+        ws = (W_Q, W_K, W_W)
+        key = (id(W_Q), id(W_K), id(W_W), dtype)
+        hit = self._entries.get(key)
+        if hit is not None:
+            refs, states, wc = hit
+            if all(r() is W for r, W in zip(refs, ws)) and \
+                    states == tuple(self._state(W) for W in ws):
+                self._entries.move_to_end(key)
+                return wc
+            del self._entries[key]
+        wc = fuse_projection_weights(W_Q, W_K, W_W, dtype)
+        entries = self._entries
+
+        def _drop(dead, key=key):
+            # a weight of this entry was collected: the entry can never hit again
+            e = entries.get(key)
+            if e is not None and any(r is dead for r in e[0]):
+                del entries[key]
+
+        refs = tuple(weakref.ref(W, _drop) for W in ws)
+        self._entries[key] = (refs, tuple(self._state(W) for W in ws), wc)
+        while len(self._entries) > self.capacity:
+            self._entries.popitem(last=False)
+        return wc
+
+    def clear(self) -> None:
+        self._entries.clear()
+
+    def __len__(self) -> int:
+        return len(self._entries)
 
 
-def _fused_weights(W_Q, W_K, W_W, dtype):
-    """[W_Q | W_K | W_W | 0-pad] as one [D, n] matrix, cached per weight
-    tensors (and their in-place versions).  The zero columns pad each row of
-    the projection output to a 16-byte multiple."""
-    key = tuple((W.data_ptr(), W._version, tuple(W.shape)) for W in (W_Q, W_K, W_W)) + (dtype,)
-    wc = _WCAT_CACHE.get(key)
-    if wc is None:
-        D = W_Q.shape[0]
-        n = W_Q.shape[1] + W_K.shape[1] + W_W.shape[1]
-        per16 = 16 // torch.tensor([], dtype=dtype).element_size()
-        n_pad = (n + per16 - 1) // per16 * per16
-        wc = torch.zeros(D, n_pad, device=W_Q.device, dtype=dtype)
-        wc[:, :n].copy_(torch.cat([W_Q, W_K, W_W], dim=1))
-        _WCAT_CACHE.clear()  # keep one entry: weights of the layer in use
-        _WCAT_CACHE[key] = wc
+def fuse_projection_weights(W_Q, W_K, W_W, dtype=None) -> torch.Tensor:
+    """[W_Q | W_K | W_W | 0-pad] as one [D, n_pad] matrix in `dtype` (default:
+    the weights' common dtype).  The zero columns pad each row of the
+    projection output to a 16-byte multiple.  Pass the result as `W_cat` to
+    indexer_from_hidden to skip the per-call cache lookup."""
+    if dtype is None:
+        dtype = L.common_dtype(W_Q, W_K, W_W)
+    D = W_Q.shape[0]
+    n = W_Q.shape[1] + W_K.shape[1] + W_W.shape[1]
+    per16 = 16 // torch.tensor([], dtype=dtype).element_size()
+    n_pad = (n + per16 - 1) // per16 * per16
+    wc = torch.zeros(D, n_pad, device=W_Q.device, dtype=dtype)
+    wc[:, :n].copy_(torch.cat([W_Q, W_K, W_W], dim=1))
     return wc
 
 
+_WCAT_CACHE = _ProjectionWeightCache()
+
+
+def _fused_weights(W_Q, W_K, W_W, dtype):
+    """The cached concatenation of one set of projection weights."""
+    return _WCAT_CACHE.get(W_Q, W_K, W_W, dtype)
+
+
 def indexer_from_hidden(h, W_Q, W_K, W_W, num_heads, head_dim, *,
-                        write_upper: bool = True) -> torch.Tensor:
+                        write_upper: bool = True,
+                        W_cat: torch.Tensor | None = None) -> torch.Tensor:
     """Projection front end fused into the indexer's input stage: ONE GEMM
     h @ [W_Q | W_K | W_W] (hipBLASLt via torch) writes every token's q, k and
     w side by side, and the MFMA indexer reads them in place through row
     strides (dsa_indexer_scores_strided) -- no split, no copies.  Same result
     as project() + indexer_scores_hip (reference lightning_indexer.py:36-47,
-    128-130)."""
+    128-130).
+
+    W_cat: the concatenated weights from fuse_projection_weights (optional;
+    without it the concatenation is looked up in, or added to, a cache keyed
+    on the weight tensors' identity and in-place version)."""
     L.require_gpu(h, W_Q, W_K, W_W)
     B, T, D = h.shape
     H, d = num_heads, head_dim
     assert W_Q.shape == (D, H * d) and W_K.shape == (D, d) and W_W.shape == (D, H), \
         "projection weight shapes"
     dt = L.common_dtype(h, W_Q, W_K, W_W)
-    wc = _fused_weights(W_Q, W_K, W_W, dt)
+    if W_cat is None:
+        wc = _fused_weights(W_Q, W_K, W_W, dt)
+    else:
+        n = H * d + d + H
+        assert W_cat.shape[0] == D and W_cat.shape[1] >= n and W_cat.dtype == dt \
+            and W_cat.is_contiguous() and (W_cat.shape[1] * W_cat.element_size()) % 16 == 0, \
+            "W_cat must be fuse_projection_weights(W_Q, W_K, W_W) in the inputs' dtype"
+        wc = W_cat
     y = L.prep(h, dt).reshape(B * T, D) @ wc          # [B*T, n_pad]
     ldr = y.shape[1]
     out = torch.empty((B, T, T), device=h.device, dtype=torch.float32)

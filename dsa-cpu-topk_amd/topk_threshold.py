@@ -1,17 +1,23 @@
-"""GPU k-th-largest ("top-K threshold") -- drop-in for the reference's CPU
-extension API (topk_avx512.cpp:226-264: topk_threshold and
-topk_threshold_batch_merge), re-hosted on the MI355X radix-select.
+"""k-th largest per row ("top-K threshold") -- drop-in for the reference's
+AVX-512 extension API (topk_avx512.cpp:226-264: topk_threshold and
+topk_threshold_batch_merge).
 
 Same contract: scores fp32, contiguous, k > 0, k <= N; returns the k-th
 largest of each row of the last dimension (ties counted) as a tensor of
 shape sizes[:-1] + [1] -- bit-identical to torch.topk(x, k).values[..., -1:].
-Same error class: RuntimeError (the extension's TORCH_CHECK).  The only
-difference is where the tensor lives: here it must be on the GPU (the
-reference's must be on the CPU).
+Same error class: RuntimeError (the extension's TORCH_CHECK).
+
+Where it runs is where the tensor lives, and nothing crosses over:
+  * GPU tensors: the MI355X radix-select (libdsa_amd.so);
+  * CPU tensors: the host library of the CPU-offload path (libdsa_cpu.so,
+    AVX-512 scan + vector quickselect on OpenMP threads) -- the reference's
+    extension takes CPU tensors, and its callers (dsa_hybrid.py:61) pass the
+    pinned host copy of the scores.
+A GPU tensor never runs on the host, and a missing library raises.
 
 Extras the reference lacks: `topk_indices` (the exactly-k index set, lowest
-index winning ties) and a `causal` mode for [B,T,T] indexer matrices that
-reads only the s <= t entries of each row.
+index winning ties; GPU) and a `causal` mode for [B,T,T] indexer matrices
+that reads only the s <= t entries of each row (both devices).
 """
 from __future__ import annotations
 
@@ -25,8 +31,6 @@ def _check(scores: torch.Tensor, k: int) -> int:
         raise RuntimeError("scores must be contiguous")
     if scores.dtype != torch.float32:
         raise RuntimeError("fp32 only")
-    if not scores.is_cuda:
-        raise RuntimeError("GPU tensor required (MI355X radix-select)")
     if k <= 0:
         raise RuntimeError("k must be > 0")
     if scores.dim() == 0:
@@ -38,7 +42,7 @@ def _check(scores: torch.Tensor, k: int) -> int:
 
 
 def _select(scores: torch.Tensor, k: int, causal: bool, want_idx: bool,
-            thr: torch.Tensor | None = None):
+            thr: torch.Tensor | None = None, nthreads: int = 0):
     N = _check(scores, k)
     rows = scores.numel() // N if N else 0
     causal_T = 0
@@ -51,6 +55,17 @@ def _select(scores: torch.Tensor, k: int, causal: bool, want_idx: bool,
     elif (thr.dtype != torch.float32 or not thr.is_contiguous() or thr.numel() != rows
           or thr.device != scores.device):
         raise RuntimeError("thr must be a contiguous fp32 tensor of one value per row")
+    if not scores.is_cuda:
+        if want_idx:
+            raise RuntimeError("topk_indices: GPU tensors only")
+        if rows:
+            lib = L.cpu_lib()
+            rc = lib.dsa_cpu_topk_threshold(scores.data_ptr(), rows, N, N, int(k), causal_T, 0,
+                                            thr.data_ptr(), int(nthreads))
+            if rc != 0:
+                msg = lib.dsa_cpu_last_error().decode(errors="replace")
+                raise RuntimeError(f"topk_threshold: {msg}")
+        return thr, None
     idx = None
     if want_idx:
         idx = torch.empty(scores.shape[:-1] + (k,), device=scores.device, dtype=torch.int32)
@@ -64,26 +79,29 @@ def _select(scores: torch.Tensor, k: int, causal: bool, want_idx: bool,
     return thr, idx
 
 
-def topk_threshold(scores: torch.Tensor, k: int, causal: bool = False) -> torch.Tensor:
+def topk_threshold(scores: torch.Tensor, k: int, causal: bool = False,
+                   nthreads: int = 0) -> torch.Tensor:
     """k-th largest of every row of the last dim -> shape [..., 1] fp32.
 
     causal=True treats a [..., T, T] matrix as causal indexer scores: row t
     reads only entries s <= t and counts the rest as -inf (what the
     reference's masked full row holds), halving the bytes read.
+    nthreads: host threads for a CPU tensor (0 = OMP_NUM_THREADS / all).
     """
-    return _select(scores, k, causal, False)[0]
+    return _select(scores, k, causal, False, nthreads=nthreads)[0]
 
 
 def topk_threshold_into(scores: torch.Tensor, k: int, thr: torch.Tensor,
-                        causal: bool = False) -> torch.Tensor:
+                        causal: bool = False, nthreads: int = 0) -> torch.Tensor:
     """topk_threshold writing into a preallocated fp32 tensor of one value
-    per row (no allocation: for pipelines that reuse their buffers)."""
-    return _select(scores, k, causal, False, thr)[0]
+    per row, on the scores' device (no allocation: for pipelines that reuse
+    their buffers, e.g. the pinned thr_cpu of the CPU-offload path)."""
+    return _select(scores, k, causal, False, thr, nthreads)[0]
 
 
 def topk_threshold_batch_merge(scores: torch.Tensor, k: int) -> torch.Tensor:
     """The reference's batch-merge variant has the same contract and result
-    (topk_avx512.cpp:255-257); on the GPU there is one select kernel."""
+    (topk_avx512.cpp:255-257); each device here has one select."""
     return _select(scores, k, False, False)[0]
 
 

@@ -22,6 +22,12 @@ CONFIGS = {
     "c1_t496": (16, 496, 32, 4, 32, 4, 32, 32, torch.float32),
     # the fused kernel's largest T (16-query blocks: the most LDS it takes)
     "fused_t2048": (2, 2048, 64, 4, 32, 4, 32, 32, torch.float32),
+    # wide attention rows (more than one wave's registers hold): head-chunked
+    # gathers (fp32) and the tile kernel (16-bit) at T < 4096 (tests only)
+    "wide_f32_t512": (2, 512, 32, 4, 32, 16, 128, 128, torch.float32),
+    "wide_f32_t2048": (1, 2048, 64, 4, 32, 16, 128, 128, torch.float32),
+    "wide_bf16_t512": (1, 512, 32, 4, 32, 128, 128, 128, torch.bfloat16),
+    "wide_bf16_t2048": (1, 2048, 64, 4, 32, 128, 128, 128, torch.bfloat16),
     "c3": (4, 4096, 256, 8, 64, 8, 64, 64, torch.float32),
     "c4": (1, 16384, 2048, 64, 128, 16, 128, 128, torch.bfloat16),
 }

@@ -16,8 +16,11 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "dsa_amd.h")
 
 
-def declared_functions():
-    text = open(HEADER).read()
+CPU_HEADER = os.path.join(ROOT, "include", "dsa_cpu.h")
+
+
+def declared_functions(header=HEADER):
+    text = open(header).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(dsa_[A-Za-z0-9_]+)\s*\(", text)))
 
@@ -28,6 +31,22 @@ def test_library_exports_every_declared_symbol():
     assert len(names) >= 7, names
     for n in names:
         assert hasattr(lib, n), f"{n} declared in dsa_amd.h but not exported"
+
+
+def test_cpu_library_exports_match_its_header():
+    """libdsa_cpu.so (include/dsa_cpu.h): every declared symbol exported,
+    nothing else exported under dsa_."""
+    import subprocess
+
+    lib = L.cpu_lib()
+    names = declared_functions(CPU_HEADER)
+    assert names == ["dsa_cpu_isa", "dsa_cpu_last_error", "dsa_cpu_topk_threshold"], names
+    for n in names:
+        assert hasattr(lib, n), n
+    out = subprocess.run(["nm", "-D", "--defined-only", L.CPU_LIB_PATH], capture_output=True,
+                         text=True).stdout
+    exported = sorted({ln.split()[-1] for ln in out.splitlines() if " T dsa_" in ln})
+    assert exported == names
 
 
 def test_export_list_matches_header():
@@ -145,6 +164,42 @@ def test_sparse_attn_rejects_bad_arguments():
     assert call(a7=0)[0] == L.DSA_OK
 
 
+def test_sparse_attn_accepts_wide_rows():
+    """Rows wider than one wave's registers are accepted (head chunks, or the
+    tile kernel for 16-bit D in {64,128}); a single head wider than a wave
+    holds is not.  B = 0: validation only, nothing launched."""
+    f = L.lib().dsa_sparse_attn_threshold
+
+    def rc(dtype, HQ, DQ, DV, B=0, T=512):
+        return _rc(f, FAKE, T, FAKE, FAKE, FAKE, FAKE, dtype, B, T, HQ, DQ, DV, 0.1, FAKE, None)
+
+    assert rc(L.DSA_F32, 16, 128, 128)[0] == L.DSA_OK
+    assert rc(L.DSA_F32, 4, 512, 512)[0] == L.DSA_OK
+    assert rc(L.DSA_F32, 32, 64, 128)[0] == L.DSA_OK
+    assert rc(L.DSA_BF16, 128, 128, 128)[0] == L.DSA_OK
+    assert rc(L.DSA_BF16, 16, 256, 256)[0] == L.DSA_OK
+    assert rc(L.DSA_F16, 64, 64, 64)[0] == L.DSA_OK
+    assert rc(L.DSA_F32, 1, 2048, 2048)[0] == L.DSA_EUNSUPPORTED     # one head > 1024 fp32
+    assert rc(L.DSA_BF16, 1, 4096, 4096)[0] == L.DSA_EUNSUPPORTED    # one head > 2048 16-bit
+
+
+def test_tiled_rejects_rows_past_4gib():
+    """The tile kernel's DMA offsets are 32-bit bytes within a batch element:
+    T*HQ*D*2 >= 4 GiB is refused before any HIP call."""
+    f = L.lib().dsa_sparse_attn_threshold_tiled
+    T = 1 << 20
+    rc, msg = _rc(f, FAKE, T, FAKE, FAKE, FAKE, FAKE, L.DSA_BF16, 1, T, 16, 128, 128, 0.1,
+                  FAKE, None)
+    assert rc == L.DSA_EINVAL and "4 GiB" in msg, (rc, msg)
+    # the gather entry applies the same bound
+    rc, msg = _rc(L.lib().dsa_sparse_attn_threshold, FAKE, T, FAKE, FAKE, FAKE, FAKE,
+                  L.DSA_BF16, 1, T, 16, 128, 128, 0.1, FAKE, None)
+    assert rc == L.DSA_EINVAL and "4 GiB" in msg, (rc, msg)
+    # just under the bound is accepted (B = 0: nothing launched)
+    assert f(FAKE, T, FAKE, FAKE, FAKE, FAKE, L.DSA_BF16, 0, T, 8, 128, 128, 0.1, FAKE,
+             None) == L.DSA_OK
+
+
 def test_fused_rejects_bad_arguments():
     f = L.lib().dsa_fused_forward
     base = [FAKE] * 6 + [L.DSA_F32, 2, 64, 4, 32, 4, 32, 32, 8, 0.17, FAKE, None]
@@ -177,8 +232,10 @@ def test_topk_threshold_contract_errors():
         topk_threshold(x.t(), 2)
     with pytest.raises(RuntimeError, match="fp32"):
         topk_threshold(x.double(), 2)
-    with pytest.raises(RuntimeError, match="GPU"):
-        topk_threshold(x, 2)
+    with pytest.raises(RuntimeError, match="k must be <= N"):
+        topk_threshold(x, 17)
+    # a CPU tensor is the reference extension's own contract: the host library
+    assert torch.equal(topk_threshold(x, 2), x.topk(2, -1).values[..., -1:])
 
 
 def test_dsa_asserts_match_reference():

@@ -168,3 +168,45 @@ def test_tiled_unsupported_shapes_raise(dev):
     with pytest.raises(DSAUnsupported):     # fp32 and D = 32 have no tile kernel
         sparse_attention_hip(s.to(dev), kth(8)(s).to(dev), Q.to(dev), K.to(dev), V.to(dev),
                              tiled=True)
+
+
+# ---------------------------------------------------------------------------
+# Wide attention rows.  The reference only asserts powers of two
+# (dsa_attention.py:298-304); rows wider than one wave's registers (fp32
+# HQ*D > 1024, 16-bit HQ*D > 2048) run as head-chunked gathers, or -- 16-bit,
+# DQ = DV in {64, 128} -- on the tile kernel at any T.
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype,HQ,DQ,DV,T,k", [
+    (torch.float32, 16, 128, 128, 512, 32),     # 2 head chunks
+    (torch.float32, 16, 128, 128, 2048, 64),
+    (torch.float32, 4, 512, 512, 256, 16),      # 2 chunks of 2 heads x 512
+    (torch.float32, 32, 64, 128, 256, 20),      # DQ != DV, 4 chunks
+    (torch.bfloat16, 128, 128, 128, 512, 32),   # tile kernel at T < 4096
+    (torch.bfloat16, 128, 128, 128, 2048, 64),
+    (torch.bfloat16, 16, 256, 256, 512, 32),    # no tile kernel for D=256: 2 chunks
+    (torch.float16, 64, 64, 64, 256, 24),       # tile kernel, f16
+])
+def test_wide_rows_threshold_wrapper(dev, dtype, HQ, DQ, DV, T, k):
+    """sparse_attention_with_threshold_triton on wide rows vs the float64
+    oracle (1e-4 fp32, 2e-2 16-bit), sampled rows at T = 2048."""
+    from helpers import sample_rows
+
+    B = 1
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    say(f"wide attn B={B} T={T} HQ={HQ} DQ={DQ} DV={DV} {dtype}")
+    _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, HQ, DQ, DV, dtype=dtype, seed0=3)
+    g = torch.Generator().manual_seed(29)
+    scores = torch.randn(B, T, T, generator=g)
+    thr = kth(k)(scores)
+    out = sparse_attention_with_threshold_triton(scores.to(dev), thr.to(dev), Q.to(dev),
+                                                 K.to(dev), V.to(dev))
+    torch.cuda.synchronize()
+    rows = None if T <= 512 else sample_rows(T, 48, seed=1, include=(0, 1, k - 1, k, T - 1))
+    if rows is None:
+        want = O.sparse_attn_threshold(scores, thr, Q, K, V)
+        got = out.cpu()
+    else:
+        want = O.sparse_attn_threshold(scores[:, rows], thr[:, rows], Q, K, V, rows=rows)
+        got = out[:, rows].cpu()
+    ok, err, _ = close(got, want, tol, tol)
+    assert ok, f"max abs err {err}"

@@ -183,3 +183,24 @@ def test_hybrid_path_with_reference_cpu_threshold(dev):
         assert torch.equal(ref.topk_threshold(s.cpu().contiguous(), k), thr_cpu)
     out = D.sparse_attention_with_threshold_triton(s, thr_cpu.to(dev), *g[3:])
     assert torch.equal(out, split)
+
+
+@pytest.mark.parametrize("name", ["wide_f32_t512", "wide_f32_t2048", "wide_bf16_t512",
+                                  "wide_bf16_t2048"])
+def test_wide_attention_rows(dev, name):
+    """dsa_attention_split_triton / dsa_attention_triton on attention rows
+    wider than one wave holds (fp32 HQ=16 x D=128, bf16 HQ=128 x D=128): the
+    reference accepts them (powers of two only, dsa_attention.py:202-206,
+    :338-340).  Staged against the oracle as for the configs."""
+    from helpers import sample_rows
+
+    ins, k = inputs(name)
+    B, T = ins[3].shape[:2]
+    tol = 1e-4 if ins[3].dtype == torch.float32 else 2e-2
+    rows = None if T <= 512 else sample_rows(T, 48, seed=2, include=(0, k - 1, k, T - 1))
+    staged_check(dev, name, rows=rows, rtol=tol, atol=tol)
+    g = to_dev(ins, dev)
+    a = D.dsa_attention_split_triton(*g, top_k=k)
+    b = D.dsa_attention_triton(*g, top_k=k)        # no fused instance: the split kernels
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)

@@ -228,3 +228,36 @@ def test_projection_front_end_fused(dev, dtype, tol):
     scale = float(ref[:, causal].abs().max())
     assert err <= tol * max(1.0, scale), f"max abs err {err} (scale {scale})"
     assert bool(torch.isneginf(out[:, ~causal]).all())
+
+
+def test_projection_weights_replaced_between_calls(dev):
+    """indexer_triton with weight set A, then A freed and set B of the same
+    shape and dtype (the caching allocator tends to hand B A's blocks): each
+    call must match the float64 oracle of its own weights (1e-3, the
+    reference's projection tolerance, test_indexer.py:36-48)."""
+    import gc
+
+    B, T, D, H, d = 2, 96, 128, 4, 64
+    causal = torch.ones(T, T, dtype=torch.bool).tril()
+    h = torch.randn(B, T, D, generator=torch.Generator().manual_seed(21))
+    hd = h.to(dev)
+    reused = 0
+    last_ptrs = None
+    for trial in range(4):
+        g = torch.Generator().manual_seed(100 + trial)
+        Ws = [torch.randn(D, n, generator=g) * 0.06 for n in (H * d, d, H)]
+        Wd = [W.to(dev) for W in Ws]
+        ptrs = tuple(W.data_ptr() for W in Wd)
+        same = ptrs == last_ptrs
+        reused += same
+        last_ptrs = ptrs
+        say(f"projection weights trial {trial} (same addresses as before: {same})")
+        out = indexer_triton(hd, *Wd, H, d).cpu()
+        hq, hk, hw = (h.double() @ W.double() for W in Ws)
+        ref = O.indexer_scores(hq.view(B, T, H, d), hk, hw)
+        err = float((out[:, causal].double() - ref[:, causal]).abs().max())
+        scale = float(ref[:, causal].abs().max())
+        assert err <= 1e-3 * max(1.0, scale), f"trial {trial}: max abs err {err} (scale {scale})"
+        del Wd, out
+        gc.collect()
+    say(f"weights landed at the previous set's addresses in {reused} of 3 replacements")

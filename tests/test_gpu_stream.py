@@ -84,3 +84,14 @@ def test_stream_graph_replays_match_eager(dev):
         for bt, o in zip(batches, sg.outputs):
             assert torch.equal(o, dsa_split_hip(*bt, k)), f"replay {rep}"
         torch.cuda.synchronize()
+
+
+def test_stream_default_form_matches_split(dev):
+    """dsa_attention_stream's default: batches one after another on the
+    caller's stream with reused buffers."""
+    say("stream default form")
+    batches = make_batches(4, 2, 512, 4, 32, 4, 32, torch.float32, dev, seed0=50)
+    outs = dsa_attention_stream(batches, top_k=32)
+    assert len({o.data_ptr() for o in outs}) == len(outs), "each batch gets its own output"
+    for bt, o in zip(batches, outs):
+        assert torch.equal(o, dsa_split_hip(*bt, 32))
