@@ -45,6 +45,8 @@ _SIGNATURES = {
                                    _P, _P], _I),
     "dsa_sparse_attn_threshold_tiled": ([_P, _I64, _P, _P, _P, _P, _I, _I64, _I64, _I, _I, _I,
                                          _F, _P, _P], _I),
+    "dsa_sparse_attn_threshold_staged": ([_P, _I64, _P, _P, _P, _P, _I, _I64, _I64, _I, _I, _I,
+                                          _F, _P, _P], _I),
     "dsa_fused_forward": ([_P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I, _I, _I, _I, _I, _I, _F,
                            _P, _P], _I),
 }

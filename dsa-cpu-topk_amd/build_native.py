@@ -25,7 +25,8 @@ CPU_SOURCES = ["topk_cpu.cpp"]
 # AVX-512 code is compiled per function and picked at run time) and no
 # -ffast-math (score rows hold -inf and NaN must order as torch.topk orders it).
 CXXFLAGS = ["-O3", "-std=c++17", "-fPIC", "-fopenmp", "-Wall", "-Wextra"]
-SOURCES = ["capi.cpp", "topk.hip", "indexer.hip", "sparse_attn.hip", "tile_attn.hip", "fused.hip"]
+SOURCES = ["capi.cpp", "topk.hip", "indexer.hip", "sparse_attn.hip", "tile_attn.hip",
+           "staged_attn.hip", "fused.hip"]
 
 HIPFLAGS = [
     "--offload-arch=gfx950",

@@ -180,6 +180,23 @@ int dsa_sparse_attn_threshold_tiled(const float* scores, int64_t ld, const float
                     "dsa_sparse_attn_threshold_tiled");
 }
 
+int dsa_sparse_attn_threshold_staged(const float* scores, int64_t ld, const float* thr,
+                                     const void* Q, const void* K, const void* V, int dtype,
+                                     int64_t B, int64_t T, int HQ, int DQ, int DV, float scale,
+                                     float* out, void* stream) {
+  int rc = check_attn(dtype, B, T, HQ, DQ, DV, Q, K, V, out, "sparse_attn_staged");
+  if (rc != DSA_OK) return rc;
+  if (!dsa::staged_attn_supported(dtype, HQ, DQ, DV))
+    return fail(DSA_EUNSUPPORTED, "sparse_attn_staged: needs DQ = DV and HQ*DQ = 256 or 512 (fp32) / 512 (16-bit) (HQ=%d DQ=%d DV=%d dtype %d)", HQ, DQ, DV, dtype);
+  if (ld < T) return fail(DSA_EINVAL, "sparse_attn_staged: ld=%lld < T=%lld", (long long)ld, (long long)T);
+  if (!std::isfinite(scale)) return fail(DSA_EINVAL, "sparse_attn_staged: scale must be finite");
+  if (B * T == 0) return DSA_OK;
+  if (!scores || !thr) return fail(DSA_EINVAL, "sparse_attn_staged: null pointer");
+  return hip_status(dsa::launch_staged_attn(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, scale,
+                                            out, static_cast<hipStream_t>(stream)),
+                    "dsa_sparse_attn_threshold_staged");
+}
+
 int dsa_fused_forward(const void* q_idx, const void* k_idx, const void* w_idx, const void* Q,
                       const void* K, const void* V, int dtype, int64_t B, int64_t T, int HI,
                       int DI, int HQ, int DQ, int DV, int top_k, float scale, float* out,

@@ -44,6 +44,16 @@ hipError_t launch_tile_attn(const float* scores, int64_t ld, const float* thr, c
                             const void* K, const void* V, int dtype, int64_t B, int64_t T, int HQ,
                             int D, float scale, float* out, hipStream_t stream);
 
+// The same attention with each block's causal K/V rows staged through LDS
+// (staged_attn.hip): rows of 64*E elements, DQ = DV, E in {4, 8} for fp32
+// and 8 for 16-bit.  The threshold entry point switches to it at
+// T >= kStagedMinT when it applies and the tile kernel does not.
+constexpr int64_t kStagedMinT = 3072;  // fp32 HQ=8,D=64: gathers win at T=2047 (0.31 vs 0.38 ms), staged at 4096 (0.54 vs 0.69)
+bool staged_attn_supported(int dtype, int HQ, int DQ, int DV);
+hipError_t launch_staged_attn(const float* scores, int64_t ld, const float* thr, const void* Q,
+                              const void* K, const void* V, int dtype, int64_t B, int64_t T,
+                              int HQ, int DQ, float scale, float* out, hipStream_t stream);
+
 // Fused forward for T <= kFusedMaxT.
 constexpr int64_t kFusedMaxT = 2048;
 hipError_t launch_fused(const void* qi, const void* ki, const void* wi, const void* Q,

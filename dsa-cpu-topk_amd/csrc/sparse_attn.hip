@@ -149,6 +149,10 @@ hipError_t launch_sparse_attn(const float* scores, int64_t ld, const float* thr,
   // head chunks (each chunk re-reads the score row and the list).
   if ((T >= kTiledMinT || nchunk > 1) && tile_attn_supported(dtype, HQ, DQ, DV, Q, K, V))
     return launch_tile_attn(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, scale, out, stream);
+  // Long rows whose K/V rows a wave holds in one slice: each block streams
+  // its causal keys once through LDS instead of gathering per query.
+  if (T >= kStagedMinT && staged_attn_supported(dtype, HQ, DQ, DV))
+    return launch_staged_attn(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, scale, out, stream);
   return launch_sparse_attn_gather(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, DV, scale,
                                    out, stream);
 }

@@ -75,14 +75,16 @@ def _attn_inputs(Q, K, V):
 
 
 def sparse_attention_hip(scores: torch.Tensor, threshold: torch.Tensor, Q, K, V,
-                         out: torch.Tensor | None = None, tiled: bool = False) -> torch.Tensor:
+                         out: torch.Tensor | None = None, tiled: bool = False,
+                         kernel: str | None = None) -> torch.Tensor:
     """Sparse attention for any T given scores [B,T,T] fp32 and threshold
     [B,T,1] (or [B,T]); only entries s <= t of each score row are read.
 
-    The library picks the kernel: per-query gathers, or -- for T >= 4096
-    with 16-bit Q/K/V and DQ = DV in {64, 128} -- dense-masked MFMA tiles.
-    tiled=True runs the tile kernel at any T (AssertionError for shapes it
-    does not cover)."""
+    The library picks the kernel: per-query gathers; dense-masked MFMA tiles
+    for T >= 4096 with 16-bit Q/K/V and DQ = DV in {64, 128}; K/V staged
+    through LDS for other long rows it covers (T >= 3072).
+    kernel="tiled" (or tiled=True) / "staged" runs that kernel at any T
+    (AssertionError for shapes it does not cover)."""
     L.require_gpu(scores, threshold, Q, K, V)
     B, T, _ = scores.shape
     HQ, DQ = Q.shape[-2], Q.shape[-1]
@@ -95,7 +97,11 @@ def sparse_attention_hip(scores: torch.Tensor, threshold: torch.Tensor, Q, K, V,
     dt, Q, K, V = _attn_inputs(Q, K, V)
     if out is None:
         out = torch.empty(B, T, HQ, DV, device=Q.device, dtype=torch.float32)
-    fn = L.lib().dsa_sparse_attn_threshold_tiled if tiled else L.lib().dsa_sparse_attn_threshold
+    if tiled:
+        kernel = "tiled"
+    fn = {None: L.lib().dsa_sparse_attn_threshold,
+          "tiled": L.lib().dsa_sparse_attn_threshold_tiled,
+          "staged": L.lib().dsa_sparse_attn_threshold_staged}[kernel]
     rc = fn(
         scores.data_ptr(), T, thr.data_ptr(), Q.data_ptr(), K.data_ptr(), V.data_ptr(),
         L.dtype_code(dt), B, T, HQ, DQ, DV, 1.0 / math.sqrt(DQ), out.data_ptr(),

@@ -15,15 +15,15 @@ pytestmark = pytest.mark.gpu
 
 
 def run_case(dev, B, T, HQ, DQ, DV, thr_fn, dtype=torch.float32, rtol=1e-4, atol=1e-4,
-             seed0=0, rows=None, tiled=False):
-    say(f"attn B={B} T={T} HQ={HQ} DQ={DQ} DV={DV} {dtype} tiled={tiled}")
+             seed0=0, rows=None, tiled=False, kernel=None):
+    say(f"attn B={B} T={T} HQ={HQ} DQ={DQ} DV={DV} {dtype} tiled={tiled} kernel={kernel}")
     _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, HQ, DQ, DV, dtype=dtype, seed0=seed0)
     g = torch.Generator().manual_seed(seed0 + 17)
     scores = torch.randn(B, T, T, generator=g)
     scores = torch.where(torch.rand(B, T, T, generator=g) < 0.1, 0.0, scores)   # ties at 0
     thr = thr_fn(scores)
     out = sparse_attention_hip(scores.to(dev), thr.to(dev), Q.to(dev), K.to(dev), V.to(dev),
-                               tiled=tiled)
+                               tiled=tiled, kernel=kernel)
     torch.cuda.synchronize()
     if rows is None:
         want = O.sparse_attn_threshold(scores, thr, Q, K, V)
@@ -210,3 +210,93 @@ def test_wide_rows_threshold_wrapper(dev, dtype, HQ, DQ, DV, T, k):
         got = out[:, rows].cpu()
     ok, err, _ = close(got, want, tol, tol)
     assert ok, f"max abs err {err}"
+
+
+# ---------------------------------------------------------------------------
+# Staged kernel (K/V streamed through LDS per block of two 32-query tiles),
+# forced at small T; the threshold entry point takes it for T >= 2048.
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("B,T,HQ,D,k,dtype", [
+    (1, 64, 8, 64, 8, torch.float32),       # two tiles, one pair
+    (2, 96, 8, 64, 12, torch.float32),      # three tiles: the middle one alone
+    (3, 200, 4, 64, 20, torch.float32),     # ragged T (not a multiple of 16 or 32)
+    (1, 333, 8, 32, 40, torch.float32),     # E = 4 (row of 256), 8 lanes per head
+    (2, 130, 2, 128, 16, torch.float32),    # E = 4, 32 lanes per head
+    (1, 257, 1, 256, 30, torch.float32),    # one head of 256 (64 lanes per head)
+    (2, 300, 8, 64, 40, torch.bfloat16),
+    (1, 190, 4, 128, 25, torch.float16),
+])
+def test_staged_kth_threshold(dev, B, T, HQ, D, k, dtype):
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    run_case(dev, B, T, HQ, D, D, kth(k), dtype=dtype, rtol=tol, atol=tol, kernel="staged")
+
+
+def test_staged_external_thresholds(dev):
+    # -inf: every causal key (dense causal attention)
+    run_case(dev, 2, 150, 8, 64, 64, lambda s: torch.full(s.shape[:2] + (1,), -math.inf),
+             kernel="staged")
+    # the diagonal score: keeps the keys scoring >= the s = t one
+    run_case(dev, 2, 150, 8, 64, 64, lambda s: s.diagonal(0, 1, 2)[..., None].contiguous(),
+             kernel="staged")
+
+
+def test_staged_empty_rows_nan_and_large_logits(dev):
+    """A NaN threshold selects nothing: NaN output, as the reference.  Large
+    logits (Q, K scaled by 8) exercise the running-max rescale."""
+    B, T, HQ, D = 1, 120, 8, 64
+    _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, HQ, D, D, seed0=4)
+    g = torch.Generator().manual_seed(6)
+    scores = torch.randn(B, T, T, generator=g)
+    thr = kth(10)(scores)
+    thr[0, 5] = math.nan
+    thr[0, 77] = math.nan
+    out = sparse_attention_hip(scores.to(dev), thr.to(dev), (Q * 8).to(dev), (K * 8).to(dev),
+                               V.to(dev), kernel="staged").cpu()
+    assert bool(torch.isnan(out[0, 5]).all()) and bool(torch.isnan(out[0, 77]).all())
+    keep = torch.ones(T, dtype=torch.bool)
+    keep[[5, 77]] = False
+    want = O.sparse_attn_threshold(scores, thr, Q * 8, K * 8, V)
+    ok, err, _ = close(out[:, keep], want[:, keep], 1e-4, 1e-4)
+    assert ok, f"max abs err {err}"
+
+
+def test_staged_and_gather_agree(dev):
+    """Same selection, two kernels: within fp32 rounding of each other."""
+    B, T, HQ, D = 2, 700, 8, 64
+    _, _, _, Q, K, V = (x.to(dev) for x in O.make_inputs(B, T, 1, 1, HQ, D, D, seed0=9))
+    scores = torch.randn(B, T, T, generator=torch.Generator().manual_seed(1)).to(dev)
+    thr = kth(70)(scores.cpu()).to(dev)
+    a = sparse_attention_hip(scores, thr, Q, K, V, kernel="staged")
+    b = sparse_attention_hip(scores, thr, Q, K, V)
+    torch.cuda.synchronize()
+    assert float((a - b).abs().max()) <= 1e-5
+
+
+def test_staged_auto_at_config3_shape(dev):
+    """T = 4096 fp32, HQ = 8, D = 64 (config 3's attention): the threshold
+    entry point runs the staged kernel; sampled rows against the oracle."""
+    from helpers import sample_rows
+
+    B, T, HQ, D, k = 1, 4096, 8, 64, 256
+    _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, HQ, D, D, seed0=12)
+    scores = torch.randn(B, T, T, generator=torch.Generator().manual_seed(2))
+    thr = kth(k)(scores)
+    out = sparse_attention_with_threshold_triton(scores.to(dev), thr.to(dev), Q.to(dev),
+                                                 K.to(dev), V.to(dev))
+    forced = sparse_attention_hip(scores.to(dev), thr.to(dev), Q.to(dev), K.to(dev), V.to(dev),
+                                  kernel="staged")
+    torch.cuda.synchronize()
+    assert torch.equal(out, forced), "T = 4096 fp32 must take the staged kernel"
+    rows = sample_rows(T, 40, seed=3, include=(0, 1, 255, 256, 4095))
+    want = O.sparse_attn_threshold(scores[:, rows], thr[:, rows], Q, K, V, rows=rows)
+    ok, err, _ = close(out[:, rows].cpu(), want, 1e-4, 1e-4)
+    assert ok, f"max abs err {err}"
+
+
+def test_staged_unsupported_shapes_raise(dev):
+    s = torch.zeros(1, 64, 64, device=dev)
+    t = torch.zeros(1, 64, 1, device=dev)
+    for HQ, D, dt in ((4, 32, torch.float32), (8, 128, torch.float32), (8, 32, torch.bfloat16)):
+        x = torch.zeros(1, 64, HQ, D, device=dev, dtype=dt)
+        with pytest.raises(AssertionError):
+            sparse_attention_hip(s, t, x, x, x, kernel="staged")
