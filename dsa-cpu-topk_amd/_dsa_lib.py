@@ -40,6 +40,8 @@ _SIGNATURES = {
     "dsa_indexer_scores": ([_P, _P, _P, _I, _I64, _I64, _I, _I, _P, _I64, _I, _P], _I),
     "dsa_indexer_scores_strided": ([_P, _P, _P, _I, _I64, _I64, _I, _I, _I64, _I64, _I64, _P,
                                     _I64, _I, _P], _I),
+    "dsa_indexer_scores_fp8_scaled": ([_P, _P, _P, _P, _P, _I64, _I64, _I, _I, _P, _I64, _I, _P],
+                                      _I),
     "dsa_topk_threshold": ([_P, _I64, _I64, _I64, _I, _I64, _P, _P, _P], _I),
     "dsa_sparse_attn_threshold": ([_P, _I64, _P, _P, _P, _P, _I, _I64, _I64, _I, _I, _I, _F,
                                    _P, _P], _I),

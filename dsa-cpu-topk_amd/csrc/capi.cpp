@@ -120,6 +120,22 @@ int dsa_indexer_scores_strided(const void* q_idx, const void* k_idx, const void*
                     "dsa_indexer_scores_strided");
 }
 
+int dsa_indexer_scores_fp8_scaled(const void* q_idx, const void* k_idx, const void* w_idx,
+                                  const float* q_scale, const float* k_scale, int64_t B,
+                                  int64_t T, int HI, int DI, float* scores, int64_t ld,
+                                  int write_upper, void* stream) {
+  int rc = check_indexer(q_idx, k_idx, w_idx, DSA_FP8, B, T, HI, DI, scores, ld);
+  if (rc != DSA_OK || B * T == 0) return rc;
+  if ((q_scale && (reinterpret_cast<uintptr_t>(q_scale) & 3u)) ||
+      (k_scale && (reinterpret_cast<uintptr_t>(k_scale) & 3u)))
+    return fail(DSA_EINVAL, "indexer_fp8_scaled: scales must be 4-byte aligned fp32");
+  return hip_status(dsa::launch_indexer(q_idx, k_idx, w_idx, DSA_FP8, B, T, HI, DI,
+                                        static_cast<int64_t>(HI) * DI, DI, HI, scores, ld,
+                                        write_upper, static_cast<hipStream_t>(stream), q_scale,
+                                        k_scale),
+                    "dsa_indexer_scores_fp8_scaled");
+}
+
 int dsa_topk_threshold(const float* scores, int64_t rows, int64_t n, int64_t ld, int k,
                        int64_t causal_T, float* thr, int32_t* idx, void* stream) {
   if (rows < 0 || n < 0) return fail(DSA_EINVAL, "topk: negative size rows=%lld n=%lld", (long long)rows, (long long)n);

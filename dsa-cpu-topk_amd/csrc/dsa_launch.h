@@ -15,9 +15,12 @@ hipError_t launch_topk(const float* scores, int64_t rows, int64_t n, int64_t ld,
 // Lightning indexer.  dtype: 0 f32, 1 bf16, 2 f16, 3 fp8 e4m3 (w fp32).
 // ldq / ldk / ldw: elements from one token's q / k / w row to the next
 // (HI*DI, DI, HI for packed tensors; a batch element spans T rows).
+// dtype 3 only: q_scale [B*T, HI] and k_scale [B*T] fp32 positive scales
+// (either may be null), I = sum_j w * ReLU(q_scale*k_scale*<q8, k8>).
 hipError_t launch_indexer(const void* q, const void* k, const void* w, int dtype, int64_t B,
                           int64_t T, int HI, int DI, int64_t ldq, int64_t ldk, int64_t ldw,
-                          float* scores, int64_t ld, int write_upper, hipStream_t stream);
+                          float* scores, int64_t ld, int write_upper, hipStream_t stream,
+                          const float* q_scale = nullptr, const float* k_scale = nullptr);
 bool indexer_supported(int dtype, int DI);
 bool indexer_fp8_fits(int HI, int DI);  // the fp8 kernel's 4-query tile fits LDS
 

@@ -44,6 +44,10 @@ struct IndexerArgs {
   int64_t ld;
   int write_upper;
   int64_t ldq, ldk, ldw;  // elements from one token's q / k / w row to the next
+  // fp8 only (either may be null): per (token, head) scales of q [B*T, HI]
+  // and per token scales of k [B*T], fp32, positive.
+  const float* q_scale;
+  const float* k_scale;
 };
 
 template <typename Tag, int DI, int KB>
@@ -179,7 +183,11 @@ size_t qtile_lds_bytes(QTileShape sh) {
 //       (query 4*quad + r16/4, head 4*hg + r16%4), chunk `chunk` of the
 //       lane group's DI slice (lane/16 owns dims [lane/16*DI/4, ...))
 //   wf[quad][hg][g][4]        : float   w of query 4*quad+g, heads 4hg..4hg+3
-template <typename Tag, int DI, int KB, int NQ>
+// KS: fp8 with scales.  Positive scales factor out of the ReLU,
+//   w * ReLU(qs*ks*<q8,k8>) = (w*qs) * ks * ReLU(<q8,k8>),
+// so q's scale is folded into w when w is staged and k's multiplies each
+// finished score (loaded with the key block it belongs to).
+template <typename Tag, int DI, int KB, int NQ, bool KS = false>
 __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs a) {
   using raw = typename Tag::raw;
   using S = Slice<Tag, DI / 4>;
@@ -233,7 +241,10 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
       const int tl = u / hp4;
       const int h = u - tl * hp4;
       const int t = t0 + tl;
-      const float wv = (t < T && h < HI) ? weight_f32<Tag>(w[static_cast<int64_t>(t) * a.ldw + h]) : 0.f;
+      float wv = (t < T && h < HI) ? weight_f32<Tag>(w[static_cast<int64_t>(t) * a.ldw + h]) : 0.f;
+      if constexpr (KS) {
+        if (a.q_scale != nullptr && t < T && h < HI) wv *= a.q_scale[(b * T + t) * HI + h];
+      }
       wf[((tl >> 2) * nhg + (h >> 2)) * 16 + (tl & 3) * 4 + (h & 3)] = wv;
     }
   }
@@ -248,18 +259,44 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
   // super-blocks past the last one, loaded as prefetch) are clamped to row
   // T-1: their scores are never stored, and unconditional loads keep the
   // wait counts exact so the prefetch stays in flight during the MFMAs.
-  auto load_b = [&](int sbi, S (&bk)[KB]) {
+  // k's scales of a super-block: one load per lane (lane l holds key
+  // s0 + l % SB), spread to the lanes that store each key by row swaps.
+  const float* ksc = KS && a.k_scale != nullptr ? a.k_scale + b * T : nullptr;
+  auto load_b = [&](int sbi, S (&bk)[KB], float& ksr) {
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
       const int s = min(sbi * SB + 16 * kb + r16, T - 1);
       bk[kb].load(k + static_cast<int64_t>(s) * a.ldk + g * E);
+    }
+    if constexpr (KS) ksr = ksc != nullptr ? ksc[min(sbi * SB + (lane % SB), T - 1)] : 1.f;
+  };
+  // ks[kb] = scale of key s0 + 16kb + r16, from lane 16kb + r16's load
+  auto spread_ks = [&](float ksr, float (&ks)[KB]) {
+    if constexpr (!KS) {
+      (void)ksr;
+      (void)ks;
+    } else if constexpr (KB == 4) {
+      const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(ksr), __float_as_uint(ksr),
+                                                      false, false);  // rows {0,1} / {2,3} of l
+      const auto lo = __builtin_amdgcn_permlane16_swap(x[0], x[0], false, false);
+      const auto hi = __builtin_amdgcn_permlane16_swap(x[1], x[1], false, false);
+      ks[0] = __uint_as_float(lo[0]);
+      ks[1] = __uint_as_float(lo[1]);
+      ks[2] = __uint_as_float(hi[0]);
+      ks[3] = __uint_as_float(hi[1]);
+    } else {
+      static_assert(KB == 2, "fp8 super-blocks are 2 or 4 key blocks");
+      const auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(ksr), __float_as_uint(ksr),
+                                                      false, false);
+      ks[0] = __uint_as_float(x[0]);
+      ks[1] = __uint_as_float(x[1]);
     }
   };
 
   // All NQ quads against one super-block.  The head-group loop holds no
   // stores: a loop with stores and no loads makes the compiler drain every
   // outstanding load (the prefetch included) before entering it.
-  auto compute = [&](int sbi, const S (&bk)[KB]) {
+  auto compute = [&](int sbi, const S (&bk)[KB], float ksr) {
     const int s0 = sbi * SB;
     float sc[NQ][KB];
 #pragma unroll
@@ -301,6 +338,8 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
         }
       }
     }
+    float ks[KB];
+    if constexpr (KS) spread_ks(ksr, ks);
 #pragma unroll
     for (int qd = 0; qd < NQ; ++qd) {
       const int tq = t0 + 4 * qd + g;  // this lane's output query
@@ -308,8 +347,10 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
           const int s = s0 + 16 * kb + r16;
+          float v = sc[qd][kb];
+          if constexpr (KS) v *= ks[kb];
           if (s < T && (s <= tq || a.write_upper))
-            out[static_cast<int64_t>(tq) * a.ld + s] = (s <= tq) ? sc[qd][kb] : ninf;
+            out[static_cast<int64_t>(tq) * a.ld + s] = (s <= tq) ? v : ninf;
         }
       }
     }
@@ -318,15 +359,16 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
   // Ping-pong over two register sets: compute on one while the other loads.
   const int last = nsb - 1;
   S b0[KB], b1[KB];
+  float k0s = 1.f, k1s = 1.f;  // k's scales (KS only; otherwise unused)
   int sb = wave;
-  load_b(min(sb, last), b0);
+  load_b(min(sb, last), b0, k0s);
   while (sb < nsb) {
-    load_b(min(sb + kQWaves, last), b1);
-    compute(sb, b0);
+    load_b(min(sb + kQWaves, last), b1, k1s);
+    compute(sb, b0, k0s);
     sb += kQWaves;
     if (sb >= nsb) break;
-    load_b(min(sb + kQWaves, last), b0);
-    compute(sb, b1);
+    load_b(min(sb + kQWaves, last), b0, k0s);
+    compute(sb, b1, k1s);
     sb += kQWaves;
   }
 
@@ -344,9 +386,9 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
   }
 }
 
-template <typename Tag, int DI, int KB, int NQ>
+template <typename Tag, int DI, int KB, int NQ, bool KS = false>
 hipError_t launch_qtile(const IndexerArgs& a, QTileShape sh, hipStream_t stream) {
-  auto kern = indexer_qtile_kernel<Tag, DI, KB, NQ>;
+  auto kern = indexer_qtile_kernel<Tag, DI, KB, NQ, KS>;
   const size_t lds = qtile_lds_bytes<Tag, DI>(sh);
   static const bool attr_set = [&] {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -382,6 +424,16 @@ hipError_t launch_stream(const IndexerArgs& a, hipStream_t stream);
 template <typename Tag, int DI, int KB>
 hipError_t launch(const IndexerArgs& a, hipStream_t stream) {
   const QTileShape sh = pick_qtile<Tag, DI>(a);
+  if constexpr (__is_same(Tag, FP8)) {
+    if (a.q_scale != nullptr || a.k_scale != nullptr) {
+      switch (sh.nq) {
+        case 4: return launch_qtile<Tag, DI, KB, 4, true>(a, sh, stream);
+        case 2: return launch_qtile<Tag, DI, KB, 2, true>(a, sh, stream);
+        case 1: return launch_qtile<Tag, DI, KB, 1, true>(a, sh, stream);
+      }
+      return hipErrorNotSupported;
+    }
+  }
   switch (sh.nq) {
     case 4: return launch_qtile<Tag, DI, KB, 4>(a, sh, stream);
     case 2: return launch_qtile<Tag, DI, KB, 2>(a, sh, stream);
@@ -444,9 +496,12 @@ bool indexer_fp8_fits(int HI, int DI) {
 
 hipError_t launch_indexer(const void* q, const void* k, const void* w, int dtype, int64_t B,
                           int64_t T, int HI, int DI, int64_t ldq, int64_t ldk, int64_t ldw,
-                          float* scores, int64_t ld, int write_upper, hipStream_t stream) {
+                          float* scores, int64_t ld, int write_upper, hipStream_t stream,
+                          const float* q_scale, const float* k_scale) {
   if (B == 0 || T == 0) return hipSuccess;
-  IndexerArgs a{q, k, w, B, static_cast<int>(T), HI, scores, ld, write_upper, ldq, ldk, ldw};
+  if ((q_scale != nullptr || k_scale != nullptr) && dtype != 3) return hipErrorInvalidValue;
+  IndexerArgs a{q, k, w, B, static_cast<int>(T), HI, scores, ld, write_upper, ldq, ldk, ldw,
+                q_scale, k_scale};
   switch (dtype) {
     case 0: return dispatch_di<F32>(a, DI, stream);
     case 1: return dispatch_di<BF16>(a, DI, stream);

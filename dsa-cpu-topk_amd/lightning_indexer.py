@@ -51,14 +51,19 @@ def indexer_torch(h, W_Q, W_K, W_W, num_heads, head_dim):
 # MI355X kernel (replaces _indexer_score_kernel + indexer_scores_triton, :54-125)
 # ---------------------------------------------------------------------------
 def indexer_scores_hip(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor, *,
-                       write_upper: bool = True, out: torch.Tensor | None = None) -> torch.Tensor:
+                       write_upper: bool = True, out: torch.Tensor | None = None,
+                       q_scale: torch.Tensor | None = None,
+                       k_scale: torch.Tensor | None = None) -> torch.Tensor:
     """Indexer scores [B,T,T] fp32 from the gfx950 MFMA kernel.
 
     write_upper=False leaves the s > t triangle untouched (the split pipeline
     never reads it).  `out` may be a preallocated [B,T,T] fp32 buffer.
 
-    q and k both torch.float8_e4m3fn select the fp8 MFMA kernel (unscaled
-    E4M3 operands, exact products, fp32 accumulation; w is taken as fp32).
+    q and k both torch.float8_e4m3fn select the fp8 MFMA kernel (E4M3
+    operands, exact products, fp32 accumulation; w is taken as fp32), with
+    optional positive quantisation scales q_scale [B,T,H] (per token and
+    head) and k_scale [B,T] (per token): the scores are then those of the
+    dequantised q_scale*q and k_scale*k (dsa_indexer_scores_fp8_scaled).
     The reference has no fp8 path: its kernel upcasts every load to fp32
     (lightning_indexer.py:81-91), which fp8 inputs match to fp32 rounding.
     """
@@ -66,6 +71,31 @@ def indexer_scores_hip(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor, *,
     B, T, H, d = q.shape
     assert k.shape == (B, T, d), f"k shape {tuple(k.shape)} != {(B, T, d)}"
     assert w.shape == (B, T, H), f"w shape {tuple(w.shape)} != {(B, T, H)}"
+    if q_scale is not None or k_scale is not None:
+        assert q.dtype == torch.float8_e4m3fn and k.dtype == torch.float8_e4m3fn, \
+            "quantisation scales go with fp8 (e4m3) q and k"
+        if q_scale is not None:
+            L.require_gpu(q_scale)
+            assert q_scale.shape == (B, T, H), f"q_scale shape {tuple(q_scale.shape)} != {(B, T, H)}"
+            q_scale = L.prep(q_scale, torch.float32)
+        if k_scale is not None:
+            L.require_gpu(k_scale)
+            assert k_scale.numel() == B * T, f"k_scale must hold B*T = {B * T} values"
+            k_scale = L.prep(k_scale.reshape(B, T), torch.float32)
+        dt = torch.float8_e4m3fn
+        q, k = L.prep(q, dt), L.prep(k, dt)
+        w = L.prep(w, torch.float32)
+        if out is None:
+            out = torch.empty((B, T, T), device=q.device, dtype=torch.float32)
+        else:
+            assert out.shape == (B, T, T) and out.dtype == torch.float32 and out.is_contiguous()
+        rc = L.lib().dsa_indexer_scores_fp8_scaled(
+            q.data_ptr(), k.data_ptr(), w.data_ptr(),
+            q_scale.data_ptr() if q_scale is not None else None,
+            k_scale.data_ptr() if k_scale is not None else None,
+            B, T, H, d, out.data_ptr(), T, 1 if write_upper else 0, L.stream_ptr(q.device))
+        L.check(rc, "indexer_scores_fp8_scaled")
+        return out
     if q.dtype == torch.float8_e4m3fn and k.dtype == torch.float8_e4m3fn:
         dt = torch.float8_e4m3fn
         q, k = L.prep(q, dt), L.prep(k, dt)

@@ -89,6 +89,30 @@ int dsa_indexer_scores_strided(const void* q_idx, const void* k_idx, const void*
                                void* stream);
 
 /*
+ * FP8 (E4M3) indexer with quantisation scales: q_idx and k_idx as e4m3 with
+ * a positive fp32 scale per (token, head) of q_idx and per token of k_idx,
+ * the layout of a block-128 (per head row) activation quantisation:
+ *   scores[b,t,s] = sum_j w[b,t,j] * ReLU(q_scale[b,t,j] * k_scale[b,s] *
+ *                                         <q8[b,t,j,:], k8[b,s,:]>)   for s <= t
+ * (-inf above the diagonal when write_upper).  With positive scales this is
+ * the indexer of the dequantised q and k; q_scale is folded into w and
+ * k_scale multiplies each finished score, so the MFMA work is the unscaled
+ * fp8 kernel's.  Either scale pointer may be NULL (scale 1).
+ *   q_scale [B,T,HI] fp32, k_scale [B,T] fp32 (contiguous, 4-byte aligned);
+ *   w_idx [B,T,HI] fp32.  Other arguments and constraints as
+ *   dsa_indexer_scores with dtype DSA_FP8.
+ * Scales must be positive and finite (a zero or negative scale does not
+ * commute with the ReLU); quantisation scales (amax / 448) are.
+ * Replaces: the scaling and dequantisation inside the indexer that the
+ *   reference lists as its FP8 follow-up (DEVLOG.md:203-205); the indexer
+ *   itself is lightning_indexer.py:54-125.
+ */
+int dsa_indexer_scores_fp8_scaled(const void* q_idx, const void* k_idx, const void* w_idx,
+                                  const float* q_scale, const float* k_scale, int64_t B,
+                                  int64_t T, int HI, int DI, float* scores, int64_t ld,
+                                  int write_upper, void* stream);
+
+/*
  * Per-row k-th largest ("top-K threshold") with an optional exactly-k index set.
  *   thr[r] = k-th largest of row r, ties counted (torch.topk(x,k).values[...,-1]).
  *   idx[r*k .. r*k+k) (optional, may be NULL) = the k positions a stable

@@ -145,6 +145,19 @@ def test_fp8_is_indexer_only():
     assert rc == L.DSA_EINVAL and "fp8" in msg
 
 
+def test_fp8_scaled_entry_checks():
+    """dsa_indexer_scores_fp8_scaled: the fp8 indexer's checks, scales 4-byte
+    aligned, null scales allowed."""
+    f = L.lib().dsa_indexer_scores_fp8_scaled
+    assert f(FAKE, FAKE, FAKE, None, None, 0, 64, 4, 128, FAKE, 64, 1, None) == L.DSA_OK
+    assert _rc(f, FAKE, FAKE, FAKE, None, None, 2, 64, 4, 32, FAKE, 64, 1, None)[0] == \
+        L.DSA_EUNSUPPORTED                                               # fp8 needs DI >= 64
+    rc, msg = _rc(f, FAKE, FAKE, FAKE, FAKE + 2, None, 2, 64, 4, 128, FAKE, 64, 1, None)
+    assert rc == L.DSA_EINVAL and "aligned" in msg
+    assert _rc(f, FAKE, FAKE, FAKE, None, None, 2, 64, 4, 128, FAKE, 32, 1, None)[0] == \
+        L.DSA_EINVAL                                                     # ld < T
+
+
 def test_sparse_attn_rejects_bad_arguments():
     f = L.lib().dsa_sparse_attn_threshold
     base = [FAKE, 64, FAKE, FAKE, FAKE, FAKE, L.DSA_F32, 2, 64, 4, 32, 32, 0.17, FAKE, None]

@@ -261,3 +261,65 @@ def test_projection_weights_replaced_between_calls(dev):
         del Wd, out
         gc.collect()
     say(f"weights landed at the previous set's addresses in {reused} of 3 replacements")
+
+
+# ---------------------------------------------------------------------------
+# fp8 with quantisation scales (dsa_indexer_scores_fp8_scaled): q quantised
+# per (token, head) row and k per token to E4M3 with scale = amax / 448, the
+# layout of a block-128 activation quantisation (the reference's fp8
+# follow-up, DEVLOG.md:203-205).  Oracle: the float64 indexer of the
+# dequantised values scale * e4m3, which is what the kernel computes
+# (positive scales factor out of the ReLU); bound as for unscaled fp8.
+# ---------------------------------------------------------------------------
+def quantise_rows(x, dim_last):
+    """e4m3 values and positive per-row scales (amax over the last dim / 448)."""
+    amax = x.abs().amax(dim=-1, keepdim=True).clamp_min(1e-12)
+    scale = amax / 448.0
+    return (x / scale).to(torch.float8_e4m3fn), scale.squeeze(-1)
+
+
+@pytest.mark.parametrize("B,T,HI,DI", [(1, 256, 64, 128), (2, 130, 4, 64), (1, 200, 12, 256)])
+def test_fp8_scaled_against_dequantised_oracle(dev, B, T, HI, DI):
+    say(f"indexer fp8 scaled B={B} T={T} HI={HI} DI={DI}")
+    q, k, w, *_ = O.make_inputs(B, T, HI, DI, 1, 1, 1, seed0=7)
+    # spread the rows' magnitudes over several binades so the scales differ
+    g = torch.Generator().manual_seed(8)
+    q = q * torch.exp2(torch.randint(-4, 5, (B, T, HI, 1), generator=g).float())
+    k = k * torch.exp2(torch.randint(-4, 5, (B, T, 1), generator=g).float())
+    q8, qs = quantise_rows(q, DI)
+    k8, ks = quantise_rows(k, DI)
+    s = indexer_scores_hip(q8.to(dev), k8.to(dev), w.to(dev), q_scale=qs.to(dev),
+                           k_scale=ks.to(dev))
+    torch.cuda.synchronize()
+    got = s.cpu()
+    want = O.indexer_scores(q8.double() * qs.double()[..., None],
+                            k8.double() * ks.double()[..., None], w)
+    causal = torch.ones(T, T, dtype=torch.bool).tril()
+    mag = float(want[:, causal].abs().max())
+    ok, err, excess = close(got[:, causal], want[:, causal], 2e-3, 2e-3 * max(1.0, mag / 10))
+    say(f"  max abs err {err:.3g} (scores up to {mag:.3g}), worst err/bound {excess:.3g}")
+    assert ok, f"max abs err {err}"
+    assert bool(torch.isneginf(got[:, ~causal]).all()), "off-causal entries must be -inf"
+
+
+def test_fp8_unit_scales_equal_unscaled(dev):
+    """Scales of 1 (either or both) give the unscaled fp8 kernel's scores
+    bit for bit."""
+    B, T, HI, DI = 2, 150, 8, 128
+    q, k, w, *_ = O.make_inputs(B, T, HI, DI, 1, 1, 1, seed0=9)
+    q8, k8 = (x.to(torch.float8_e4m3fn).to(dev) for x in (q, k))
+    w = w.to(dev)
+    base = indexer_scores_hip(q8, k8, w)
+    ones_q = torch.ones(B, T, HI, device=dev)
+    ones_k = torch.ones(B, T, device=dev)
+    for qs, ks in ((ones_q, None), (None, ones_k), (ones_q, ones_k)):
+        got = indexer_scores_hip(q8, k8, w, q_scale=qs, k_scale=ks)
+        torch.cuda.synchronize()
+        assert torch.equal(got, base)
+
+
+def test_fp8_scales_need_fp8_inputs(dev):
+    q = torch.zeros(1, 8, 4, 64, device=dev)
+    k = torch.zeros(1, 8, 64, device=dev)
+    with pytest.raises(AssertionError):
+        indexer_scores_hip(q, k, torch.zeros(1, 8, 4, device=dev), k_scale=torch.ones(1, 8, device=dev))
