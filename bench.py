@@ -659,6 +659,15 @@ def pmc_workload(args, dev):
     for _ in range(2):
         D.sparse_attention_hip(scores, thr, Q, K, V, out=out)   # the tile kernel at this T
     torch.cuda.synchronize()
+    del scores, thr, Q, K, V, out
+    # config 3: indexer (fp32), select, and 2 launches of the staged attention
+    ins = gpu_inputs(C3, torch.float32, dev, seed=3)
+    scores = indexer_scores_hip(*ins[:3], write_upper=False)
+    thr = topk_threshold(scores, C3["k"], causal=True)
+    out = torch.empty(C3["B"], C3["T"], C3["HQ"], C3["DV"], device=dev)
+    for _ in range(2):
+        D.sparse_attention_hip(scores, thr, *ins[3:], out=out)  # the staged kernel at this T
+    torch.cuda.synchronize()
     log("pmc workload done")
 
 
@@ -681,11 +690,16 @@ def main():
     ap.add_argument("--no-hybrid", action="store_true", help="skip the CPU-offload legs")
     ap.add_argument("--no-long", action="store_true",
                     help="skip the split-forward legs at configs 3 and 4")
+    ap.add_argument("--only-headline", action="store_true",
+                    help="run only the headline leg (fused config 1: warm-up, the timed "
+                         "graph and the event-timed launches) and print its JSON line; "
+                         "for a kernel-trace profile of that kernel alone")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run only the workload profiled with counters: one 256 MiB "
                          "device-to-device copy (counter calibration), then --steps eager "
                          "fused launches at config 1, the config-4 indexer, 3 causal "
-                         "selects and 2 tile-attention launches at config 4")
+                         "selects and 2 tile-attention launches at config 4, then the "
+                         "config-3 indexer, select and 2 staged-attention launches")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build has no "
@@ -708,8 +722,10 @@ def main():
     flops = indexer_flops(B, T, C1["HI"], C1["DI"]) + attention_flops(
         B, T, C1["k"], C1["HQ"], C1["DQ"], C1["DV"])
     achieved = flops / kern_s / 1e12
-    log("bench: split config 1")
-    split_s = bench_split(dev)
+    split_s = None
+    if not args.only_headline:
+        log("bench: split config 1")
+        split_s = bench_split(dev)
     out = {
         "metric": "DSA fwd ms + query tokens/s at B=16,T=512,k=32; top-K HBM GB/s vs peak",
         "value": round(value, 1),
@@ -736,9 +752,12 @@ def main():
                      "kernel": "fused_kernel<F32,32,2,2,2,16>",
                      "kernel_ms": round(kern_s * 1e3, 5),
                      "flops_per_launch": flops},
-        "split": {"ms_per_step": round(split_s * 1e3, 5),
-                  "value": round(B * T / split_s, 1), "unit": "query tokens/s"},
     }
+    if args.only_headline:
+        print(json.dumps(out), flush=True)
+        return
+    out["split"] = {"ms_per_step": round(split_s * 1e3, 5),
+                    "value": round(B * T / split_s, 1), "unit": "query tokens/s"}
     log("bench: config 2 sweep")
     out["sweep_c2"] = bench_sweep_c2(dev)
     if not args.no_select:

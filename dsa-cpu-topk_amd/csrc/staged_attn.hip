@@ -70,10 +70,28 @@ constexpr int row_bytes() { return kWave * E * Tag::kBytes; }
 template <typename Tag, int E>
 constexpr int tile_keys() { return kSlotK / row_bytes<Tag, E>(); }
 
+// LDS row layout.  A lane reads its slice of a row as E*bytes/16 chunks of
+// 16 bytes.  With one chunk per lane the row is stored as is (lane l reads
+// chunk l: 64 consecutive chunks, no bank conflict).  With two (fp32, E = 8)
+// the even chunks go to the first half of the row and the odd ones to the
+// second, so the wave's two reads are each 64 consecutive chunks too
+// (stored as is, lanes l and l+8 would hit the same banks: 48.6% of LDS
+// cycles were conflicts).
+template <typename Tag, int E>
+constexpr int chunks_per_lane() { return E * Tag::kBytes / 16; }
+
+// Logical chunk (16 bytes of the row in memory order) held at physical
+// position pc of an LDS row of cpr chunks.
+template <int CPL>
+__device__ __forceinline__ int logical_chunk(int pc, int cpr) {
+  if constexpr (CPL == 2) return pc < cpr / 2 ? 2 * pc : 2 * (pc - cpr / 2) + 1;
+  else return pc;
+}
+
 // Copies rows s0 .. s0+KT-1 of one batch element's [T, 64E] K or V into
 // dst (rows past T repeat row T-1; they are never selected) with the NT
-// threads of the block.  Chunk c of the tile (16 bytes) goes to dst + 16c:
-// each wave instruction fills 1 KiB.
+// threads of the block, in the LDS row layout above.  Physical chunk c of
+// the tile (16 bytes) lands at dst + 16c: each wave instruction fills 1 KiB.
 template <typename Tag, int E, int NT, int KT>
 __device__ __forceinline__ void dma_rows(const char* __restrict__ src, int s0, int T,
                                          DSA_LDS uint8_t* dst, int tid) {
@@ -86,23 +104,28 @@ __device__ __forceinline__ void dma_rows(const char* __restrict__ src, int s0, i
       const int c = c0 + tid;
       const int r = c / CPR;
       const uint32_t s = static_cast<uint32_t>(min(s0 + r, T - 1));
-      const uint32_t off = s * static_cast<uint32_t>(RB) + 16u * static_cast<uint32_t>(c % CPR);
+      const int lc = logical_chunk<chunks_per_lane<Tag, E>()>(c % CPR, CPR);
+      const uint32_t off = s * static_cast<uint32_t>(RB) + 16u * static_cast<uint32_t>(lc);
       __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(src + off),
                                        dst + (c0 + (tid & ~(kWave - 1))) * 16, 16, 0, 0);
     }
   }
 }
 
+// This lane's E elements of an LDS row (layout above), as fp32.
 template <typename Tag, int E>
 __device__ __forceinline__ void lds_slice(const DSA_LDS uint8_t* row, int lane, float (&v)[E]) {
   if constexpr (Tag::kBytes == 4) {
-    const DSA_LDS float* p = reinterpret_cast<const DSA_LDS float*>(row) + lane * E;
-#pragma unroll
-    for (int i = 0; i < E; i += 4) {
-      const f32x4 f = *reinterpret_cast<const DSA_LDS f32x4*>(p + i);
-      v[i] = f[0]; v[i + 1] = f[1]; v[i + 2] = f[2]; v[i + 3] = f[3];
+    static_assert(E == 4 || E == 8, "one or two chunks per lane");
+    const DSA_LDS f32x4* p = reinterpret_cast<const DSA_LDS f32x4*>(row);
+    const f32x4 f = p[lane];
+    v[0] = f[0]; v[1] = f[1]; v[2] = f[2]; v[3] = f[3];
+    if constexpr (E == 8) {
+      const f32x4 h = p[kWave + lane];  // odd chunks: second half of the row
+      v[4] = h[0]; v[5] = h[1]; v[6] = h[2]; v[7] = h[3];
     }
   } else {
+    static_assert(E == 8, "one chunk per lane");
     const DSA_LDS uint16_t* p = reinterpret_cast<const DSA_LDS uint16_t*>(row) + lane * E;
 #pragma unroll
     for (int i = 0; i < E; i += 8) {
