@@ -186,6 +186,7 @@ int dsa_sparse_attn_threshold_tiled(const float* scores, int64_t ld, const float
   if (T * HQ * static_cast<int64_t>(DQ) * 2 > (int64_t{1} << 32) - 1)
     return fail(DSA_EINVAL, "sparse_attn_tiled: T*HQ*D = %lld 16-bit elements must be < 4 GiB",
                 (long long)(T * HQ * static_cast<int64_t>(DQ)));
+  if (ld > dsa::kTileMaxLd) return fail(DSA_EINVAL, "sparse_attn_tiled: ld=%lld > %lld", (long long)ld, (long long)dsa::kTileMaxLd);
   if (B * T == 0) return DSA_OK;
   if (!scores || !thr || !Q || !K || !V || !out) return fail(DSA_EINVAL, "sparse_attn_tiled: null pointer");
   if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(out))
@@ -194,6 +195,54 @@ int dsa_sparse_attn_threshold_tiled(const float* scores, int64_t ld, const float
   return hip_status(dsa::launch_tile_attn(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, scale,
                                           out, static_cast<hipStream_t>(stream)),
                     "dsa_sparse_attn_threshold_tiled");
+}
+
+int dsa_selection_mask(const float* scores, int64_t ld, const float* thr, int64_t B, int64_t T,
+                       uint64_t* mask, int64_t ldm, void* stream) {
+  if (B < 0 || T < 0) return fail(DSA_EINVAL, "selection_mask: negative size");
+  if (T > kMaxElems) return fail(DSA_EINVAL, "selection_mask: T=%lld too large", (long long)T);
+  if (ld < T) return fail(DSA_EINVAL, "selection_mask: ld=%lld < T=%lld", (long long)ld, (long long)T);
+  if (ldm < (T + 63) / 64)
+    return fail(DSA_EINVAL, "selection_mask: ldm=%lld < ceil(T/64)=%lld", (long long)ldm, (long long)((T + 63) / 64));
+  if ((B * T + 3) / 4 > (int64_t{1} << 31) - 1) return fail(DSA_EINVAL, "selection_mask: B*T too large for one launch");
+  if (B * T == 0) return DSA_OK;
+  if (!scores || !thr || !mask) return fail(DSA_EINVAL, "selection_mask: null pointer");
+  if ((reinterpret_cast<uintptr_t>(mask) & 7u) != 0) return fail(DSA_EINVAL, "selection_mask: mask must be 8-byte aligned");
+  return hip_status(dsa::launch_selection_mask(scores, ld, thr, B, T, mask, ldm,
+                                               static_cast<hipStream_t>(stream)),
+                    "dsa_selection_mask");
+}
+
+int dsa_sparse_attn_mask(const uint64_t* mask, int64_t ldm, const void* Q, const void* K,
+                         const void* V, int dtype, int64_t B, int64_t T, int HQ, int DQ, int DV,
+                         float scale, float* out, void* stream) {
+  if (!dtype_ok(dtype)) return fail(DSA_EINVAL, "sparse_attn_mask: unknown dtype %d", dtype);
+  if (B < 0 || T < 0) return fail(DSA_EINVAL, "sparse_attn_mask: negative size");
+  if (T > kMaxElems) return fail(DSA_EINVAL, "sparse_attn_mask: T=%lld too large", (long long)T);
+  if (HQ < 1 || HQ > 1024) return fail(DSA_EINVAL, "sparse_attn_mask: HQ=%d outside [1,1024]", HQ);
+  if (!std::isfinite(scale)) return fail(DSA_EINVAL, "sparse_attn_mask: scale must be finite");
+  if (dtype == DSA_F32 || dtype == DSA_FP8 || DQ != DV || (DQ != 64 && DQ != 128))
+    return fail(DSA_EUNSUPPORTED, "sparse_attn_mask: needs bf16/fp16 and DQ = DV in {64,128} (dtype %d DQ=%d DV=%d)", dtype, DQ, DV);
+  if (ldm < (T + 63) / 64)
+    return fail(DSA_EINVAL, "sparse_attn_mask: ldm=%lld < ceil(T/64)=%lld", (long long)ldm, (long long)((T + 63) / 64));
+  // 128 mask rows are addressed with 32-bit byte offsets
+  if (ldm > (int64_t{1} << 21) - 1) return fail(DSA_EINVAL, "sparse_attn_mask: ldm=%lld too large", (long long)ldm);
+  if (T * HQ * static_cast<int64_t>(DQ) * 2 > (int64_t{1} << 32) - 1)
+    return fail(DSA_EINVAL, "sparse_attn_mask: T*HQ*D = %lld 16-bit elements must be < 4 GiB",
+                (long long)(T * HQ * static_cast<int64_t>(DQ)));
+  if (B * T == 0) return DSA_OK;
+  if (!mask || !Q || !K || !V || !out) return fail(DSA_EINVAL, "sparse_attn_mask: null pointer");
+  if ((reinterpret_cast<uintptr_t>(mask) & 7u) != 0) return fail(DSA_EINVAL, "sparse_attn_mask: mask must be 8-byte aligned");
+  if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(out))
+    return fail(DSA_EINVAL, "sparse_attn_mask: Q/K/V/out must be 16-byte aligned");
+  if (B * T * HQ * static_cast<int64_t>(DQ) > (int64_t{1} << 40)) return fail(DSA_EINVAL, "sparse_attn_mask: Q too large");
+  return hip_status(dsa::launch_tile_attn_mask(mask, ldm, Q, K, V, dtype, B, T, HQ, DQ, scale, out,
+                                               static_cast<hipStream_t>(stream)),
+                    "dsa_sparse_attn_mask");
+}
+
+int dsa_sparse_attn_uses_mask(int dtype, int64_t T, int HQ, int DQ, int DV) {
+  return dtype_ok(dtype) && dsa::sparse_attn_uses_tiles(dtype, T, HQ, DQ, DV) ? 1 : 0;
 }
 
 int dsa_sparse_attn_threshold_staged(const float* scores, int64_t ld, const float* thr,

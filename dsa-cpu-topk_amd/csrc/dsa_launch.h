@@ -41,11 +41,23 @@ bool sparse_attn_chunked(int dtype, int HQ, int DQ, int DV);
 // The same attention as dense-masked MFMA tiles (tile_attn.hip).  The
 // threshold entry point switches to it at T >= kTiledMinT when it applies.
 constexpr int64_t kTiledMinT = 4096;
+// The tile kernel addresses 128 score rows (fp32) with 32-bit byte offsets.
+constexpr int64_t kTileMaxLd = (int64_t{1} << 22) - 1;
+// Whether launch_sparse_attn takes the tile kernel for this shape (16-bit,
+// DQ = DV in {64, 128}, and T >= kTiledMinT or heads too wide to gather).
+bool sparse_attn_uses_tiles(int dtype, int64_t T, int HQ, int DQ, int DV);
 bool tile_attn_supported(int dtype, int HQ, int DQ, int DV, const void* Q, const void* K,
                          const void* V);
 hipError_t launch_tile_attn(const float* scores, int64_t ld, const float* thr, const void* Q,
                             const void* K, const void* V, int dtype, int64_t B, int64_t T, int HQ,
                             int D, float scale, float* out, hipStream_t stream);
+// The tile kernel reading its selection from a bitmask (selection_mask),
+// and the kernel that builds that bitmask from scores and thresholds.
+hipError_t launch_tile_attn_mask(const uint64_t* mask, int64_t ldm, const void* Q, const void* K,
+                                 const void* V, int dtype, int64_t B, int64_t T, int HQ, int D,
+                                 float scale, float* out, hipStream_t stream);
+hipError_t launch_selection_mask(const float* scores, int64_t ld, const float* thr, int64_t B,
+                                 int64_t T, uint64_t* mask, int64_t ldm, hipStream_t stream);
 
 // The same attention with each block's causal K/V rows staged through LDS
 // (staged_attn.hip): rows of 64*E elements, DQ = DV, E in {4, 8} for fp32

@@ -139,15 +139,20 @@ bool sparse_attn_supported(int dtype, int HQ, int DQ, int DV) {
   return false;
 }
 
+bool sparse_attn_uses_tiles(int dtype, int64_t T, int HQ, int DQ, int DV) {
+  if ((dtype != 1 && dtype != 2) || DQ != DV || (DQ != 64 && DQ != 128) || HQ < 1) return false;
+  return T >= kTiledMinT || head_chunks(dtype, HQ, DQ, DV) > 1;
+}
+
 hipError_t launch_sparse_attn(const float* scores, int64_t ld, const float* thr, const void* Q,
                               const void* K, const void* V, int dtype, int64_t B, int64_t T,
                               int HQ, int DQ, int DV, float scale, float* out,
                               hipStream_t stream) {
   if (B == 0 || T == 0) return hipSuccess;
-  const int nchunk = head_chunks(dtype, HQ, DQ, DV);
   // Dense-masked tiles for long rows, and for rows whose gathers would need
   // head chunks (each chunk re-reads the score row and the list).
-  if ((T >= kTiledMinT || nchunk > 1) && tile_attn_supported(dtype, HQ, DQ, DV, Q, K, V))
+  if (sparse_attn_uses_tiles(dtype, T, HQ, DQ, DV) && ld <= kTileMaxLd &&
+      tile_attn_supported(dtype, HQ, DQ, DV, Q, K, V))
     return launch_tile_attn(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, scale, out, stream);
   // Long rows whose K/V rows a wave holds in one slice: each block streams
   // its causal keys once through LDS instead of gathering per query.

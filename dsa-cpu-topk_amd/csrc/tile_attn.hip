@@ -40,8 +40,26 @@
 // uses fp32 probabilities; the difference is far inside the 16-bit
 // tolerance); everything else is fp32.  Rows that select nothing get
 // 0/0 = NaN, as the reference.
+#include <type_traits>
+
 #include "dsa_device.h"
 #include "dsa_launch.h"
+
+typedef float dsa_f32x4 __attribute__((ext_vector_type(4)));
+// Raw buffer loads of fp32 data, declared outside any namespace so that
+// the asm labels bind the intrinsics (the LLVM intrinsics, typed as float: the
+// integer-vector forms of the clang builtins are narrowed to one dword by
+// this toolchain's optimiser, which then repeats that dword in every
+// element).  Arguments: resource, byte offset (VGPR), SGPR offset, cache
+// policy.
+__device__ dsa_f32x4 buffer_load_f32x4(__amdgpu_buffer_rsrc_t rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.ptr.buffer.load.v4f32");
+__device__ float buffer_load_f32(__amdgpu_buffer_rsrc_t rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.ptr.buffer.load.f32");
+typedef float dsa_f32x2 __attribute__((ext_vector_type(2)));
+__device__ dsa_f32x2 buffer_load_f32x2(__amdgpu_buffer_rsrc_t rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.ptr.buffer.load.v2f32");
+
 
 namespace dsa {
 namespace {
@@ -62,8 +80,14 @@ struct TileArgs {
   int HQ;
   float scale_log2;
   float* out;
-  int vec;  // score rows 16-byte aligned with ld % 4 == 0: float4 loads (ld >= 4 then)
+  const uint64_t* mask;  // selection bitmask (kSrcMask): [B*T][ldm] words
+  int64_t ldm;
 };
+
+// Where a block's selection comes from.
+constexpr int kSrcScores4 = 0;  // fp32 scores + thresholds, float4 loads (16-byte rows)
+constexpr int kSrcScores1 = 1;  // the same, dword loads
+constexpr int kSrcMask = 2;     // selection bitmask (selection_mask_kernel)
 
 template <typename Tag>
 struct Mfma16x16x32;
@@ -114,51 +138,62 @@ struct TileLds {
   static __device__ __forceinline__ int swz_v(int r) { return (2 * r) & (NCH - 1); }
 };
 
-// Issue this wave's share of the DMA of one tile (rows s0 .. s0+63 of a
-// [T, HQ*D] tensor, this head's D columns) into `dst`.  Rows past T are
-// clamped to T-1 (never causal for any query).  Completion is awaited with
-// vmcnt before the barrier that publishes the tile.
-template <int D, bool IS_K>
-__device__ __forceinline__ void dma_tile(const uint16_t* __restrict__ src, int64_t rowE, int s0,
-                                         int T, DSA_LDS uint8_t* dst, int wave, int lane) {
-  using L = TileLds<D>;
-  constexpr int PER_WAVE = L::BYTES / 1024 / (kNT / kWave);  // 1 KiB DMA instructions per wave
-  // 32-bit byte offsets against the uniform base (the host keeps a batch
-  // element's K and V under 4 GiB)
-  const char* base = reinterpret_cast<const char*>(src);
-  const uint32_t rowbytes = static_cast<uint32_t>(rowE) * 2u;
+// Buffer resource over one head's K or V rows from row s1 on (`head_base`
+// is row 0 of this batch element at this head's columns).  Its size ends at
+// row T, so DMA reads of rows at or past T are range-checked by the
+// hardware and return zeros: no per-row clamp.  Those rows are never causal
+// for any query, so they are masked to -inf and their zero V rows add 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const char* head_base, int s1, int T,
+                                                          uint32_t rowbytes) {
+  const uint64_t rem = static_cast<uint64_t>(T - s1) * rowbytes;
+  const int nrec = rem > 0xffffffffull ? -1 : static_cast<int>(static_cast<uint32_t>(rem));
+  // word 3: the raw-buffer configuration of CDNA (untyped dword access)
+  return __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(head_base + static_cast<int64_t>(s1) * rowbytes), 0, nrec, 0x00020000);
+}
+
+// Issue this wave's share of the DMA of one 64-row tile into `dst`: PW
+// 1 KiB instructions (buffer_load_dwordx4 ... lds: no registers, no LDS
+// store instructions); off[i] is the lane's loop-invariant byte offset of
+// its 16-byte chunk within the tile.  Completion is awaited with vmcnt
+// before the barrier that publishes the tile.
+template <int PW>
+__device__ __forceinline__ void dma_tile(__amdgpu_buffer_rsrc_t rsrc, const uint32_t (&off)[PW],
+                                         DSA_LDS uint8_t* dst, int wave) {
 #pragma unroll
-  for (int i = 0; i < PER_WAVE; ++i) {
-    const int ins = wave * PER_WAVE + i;
-    const int P = ins * 64 + lane;  // physical chunk index this lane fills
-    const int r = P / L::NCH, pc = P % L::NCH;
-    const int lc = pc ^ (IS_K ? L::swz_k(r) : L::swz_v(r));
-    const uint32_t s = static_cast<uint32_t>(min(s0 + r, T - 1));
-    const uint32_t off = s * rowbytes + 16u * static_cast<uint32_t>(lc);
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint16_t*>(base + off),
-                                     dst + ins * 1024, 16, 0, 0);
-  }
+  for (int i = 0; i < PW; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst + (wave * PW + i) * 1024, 16,
+                                             static_cast<int>(off[i]), 0, 0, 0);
 }
 
-__device__ __forceinline__ void wait_dma_and_sync() {
-  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  block_sync_lds();
+// Wait until at most N vector-memory operations of this wave are
+// outstanding: the ones issued last (a tile's score loads) may stay in
+// flight, everything issued before them (the DMA) has completed.
+template <int N>
+__device__ __forceinline__ void wait_dma_keep() {
+  __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <typename Tag, int D, bool VEC>
+template <typename Tag, int D, int SRC>
 __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
   static_assert(D == 64 || D == 128, "head dim");
+  constexpr bool VEC = SRC == kSrcScores4;
+  constexpr bool MASK = SRC == kSrcMask;
   using M = Mfma16x16x32<Tag>;
   using L = TileLds<D>;
   constexpr int NKS = D / 32;  // k-steps of the first product
   constexpr int NDT = D / 16;  // 16-dim output tiles
+  // 16-key tiles whose K fragments are read at once (all four unless the
+  // prefetched fp32 scores leave too few registers)
+  constexpr int KJ = (D == 128 && !MASK) ? 2 : 4;
+  constexpr int VG = 4;                 // 16-dim output tiles whose V fragments are read at once
   // Two buffers per operand, as separate objects: the compiler then knows a
   // DMA into one buffer does not alias reads of the other, and keeps the
   // next tile's DMA in flight while the current tile is read.
   __shared__ __align__(16) uint8_t k0[L::BYTES], k1[L::BYTES], v0[L::BYTES], v1[L::BYTES];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS targets in SGPRs
   const int lane = lane_id();
   const int g = lane >> 4, c16 = lane & 15;
   const int T = a.T;
@@ -183,16 +218,28 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
   const int nkt = (s_hi + kKT - 1) / kKT;
   const int wave_last = min(tw + 31, T - 1);  // last query of this wave
 
-  DSA_LDS uint8_t* kb[2] = {(DSA_LDS uint8_t*)k0, (DSA_LDS uint8_t*)k1};
-  DSA_LDS uint8_t* vb[2] = {(DSA_LDS uint8_t*)v0, (DSA_LDS uint8_t*)v1};
-  dma_tile<D, true>(Kb, rowE, 0, T, kb[0], wave, lane);
-  dma_tile<D, false>(Vb, rowE, 0, T, vb[0], wave, lane);
+  // Loop-invariant DMA offsets of this wave's chunks within a tile: physical
+  // chunk P of the tile holds row P / NCH, logical chunk (P % NCH) ^ swz(row).
+  constexpr int PW = L::BYTES / 1024 / (kNT / kWave);
+  const uint32_t rowbytes = static_cast<uint32_t>(rowE) * 2u;
+  uint32_t koff[PW], voff[PW];
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    const int P = (wave * PW + i) * 64 + lane;
+    const int r = P / L::NCH, pc = P % L::NCH;
+    koff[i] = static_cast<uint32_t>(r) * rowbytes + 16u * static_cast<uint32_t>(pc ^ L::swz_k(r));
+    voff[i] = static_cast<uint32_t>(r) * rowbytes + 16u * static_cast<uint32_t>(pc ^ L::swz_v(r));
+  }
+  const char* const kbase = reinterpret_cast<const char*>(Kb);
+  const char* const vbase = reinterpret_cast<const char*>(Vb);
+  dma_tile<PW>(tile_rsrc(kbase, 0, T, rowbytes), koff, (DSA_LDS uint8_t*)k0, wave);
+  dma_tile<PW>(tile_rsrc(vbase, 0, T, rowbytes), voff, (DSA_LDS uint8_t*)v0, wave);
 
   // Q^T fragments: qf[qt][ks] = Q[query tw+16qt+c16][dims 32ks+8g .. +8].
   u32x4 qf[2][NKS];
   int tq[2];
   float thr[2];
-  const float* srow[2];
+  uint32_t soff[2];
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     tq[qt] = tw + 16 * qt + c16;
@@ -200,8 +247,17 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks)
       qf[qt][ks] = *reinterpret_cast<const u32x4*>(Qb + tl * rowE + 32 * ks + 8 * g);
-    thr[qt] = a.thr[b * T + tl];
-    srow[qt] = a.scores + (b * T + tl) * a.ld;
+    if constexpr (MASK) {
+      thr[qt] = 0.f;
+      // byte offset of the query's mask row from row t0 (< 128 rows: the
+      // host keeps 128 * ldm * 8 below 2^31)
+      soff[qt] = static_cast<uint32_t>(tl - t0) * static_cast<uint32_t>(a.ldm) * 8u;
+    } else {
+      thr[qt] = a.thr[b * T + tl];
+      // byte offset of the query's score row from row t0 (< 128 rows: the
+      // host keeps 128 * ld * 4 below 2^31), plus this lane group's 4 keys
+      soff[qt] = static_cast<uint32_t>(tl - t0) * static_cast<uint32_t>(a.ld) * 4u + 16u * g;
+    }
   }
 
   float m[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()};
@@ -229,24 +285,36 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
   }
 
   // This wave's scores of key tile kt: sv[qt][j][r] = scores[tq[qt]][s0 +
-  // 16j + 4g + r].  Always the same loads (addresses clamped into the row;
-  // entries that are not causal are masked in compute), with no branches:
-  // loads complete in order, so with a fixed count the mask waits for these
-  // loads only and not for the next tile's DMA issued behind them.
-  const int64_t s_clamp = VEC ? a.ld - 4 : a.ld - 1;
-  auto load_scores = [&](int kt, float (&sv)[2][4][4]) {
-    const int s0 = kt * kKT;
+  // 16j + 4g + r], by buffer loads against a resource over the block's score
+  // rows from key s0 on (uniform), at the lane's invariant row offset plus an
+  // immediate per j: no address arithmetic per tile.  The resource ends at
+  // the last score of the batch element, so reads past it (keys past T of
+  // the last row, never causal) return zeros; keys past T of other rows
+  // read the next row, also never causal.  Entries that are not causal are
+  // masked in make_sel.
+  const char* const sblk =
+      MASK ? reinterpret_cast<const char*>(a.mask + (b * T + t0) * a.ldm)
+           : reinterpret_cast<const char*>(a.scores + (b * T + t0) * a.ld);
+  const uint64_t sbytes = MASK ? static_cast<uint64_t>(T - t0) * static_cast<uint64_t>(a.ldm) * 8u
+                               : static_cast<uint64_t>(T - t0) * static_cast<uint64_t>(a.ld) * 4u;
+  auto load_scores = [&](int kt, float (&sv)[2][4][4]) __attribute__((always_inline)) {
+    const uint64_t s0b = static_cast<uint64_t>(kt) * kKT * 4u;
+    const uint64_t rem = sbytes - s0b;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(sblk + s0b), 0, rem > 0xffffffffull ? -1 : static_cast<int>(static_cast<uint32_t>(rem)),
+        0x00020000);
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
+      const int vo = static_cast<int>(soff[qt]);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int s = s0 + 16 * j + 4 * g;
         if constexpr (VEC) {
-          const float4 f = *reinterpret_cast<const float4*>(srow[qt] + min<int64_t>(s, s_clamp));
-          sv[qt][j][0] = f.x; sv[qt][j][1] = f.y; sv[qt][j][2] = f.z; sv[qt][j][3] = f.w;
+          const f32x4 f = buffer_load_f32x4(rs, vo + 64 * j, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sv[qt][j][r] = f[r];
         } else {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) sv[qt][j][r] = srow[qt][min<int64_t>(s + r, s_clamp)];
+          for (int r = 0; r < 4; ++r) sv[qt][j][r] = buffer_load_f32(rs, vo + 64 * j + 4 * r, 0, 0);
         }
       }
     }
@@ -279,21 +347,83 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
     return s0 <= wave_last && __ballot(any) != 0;
   };
 
+  // Interior tiles (every key below the block's first query, so below T and
+  // causal for all its queries): the selection without the causal test.
+  // Queries past T (last block of a ragged T) compute values that are never
+  // stored; each query's softmax lives in its own column.
+  auto make_sel_fast = [&](const float (&sv)[2][4][4], bool (&sel)[2][4][4]) {
+    bool any = false;
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          sel[qt][j][r] = sv[qt][j][r] >= thr[qt];  // NaN selects nothing
+          any |= sel[qt][j][r];
+        }
+    return __ballot(any) != 0;
+  };
+
+  // Bitmask source: word kt of each query's mask row (bit i = key 64kt + i
+  // selected, causality included), one 8-byte buffer load per query tile,
+  // against a resource over the block's mask rows from word kt on.
+  auto load_words = [&](int kt, uint64_t (&mw)[2]) __attribute__((always_inline)) {
+    const uint64_t w0b = static_cast<uint64_t>(kt) * 8u;
+    const uint64_t rem = sbytes - w0b;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(sblk + w0b), 0, rem > 0xffffffffull ? -1 : static_cast<int>(static_cast<uint32_t>(rem)),
+        0x00020000);
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt)
+      mw[qt] = __builtin_bit_cast(uint64_t, buffer_load_f32x2(rs, static_cast<int>(soff[qt]), 0, 0));
+  };
+  // Entry (qt, j, r) of lane group g is key 16j + 4g + r of the tile: bit
+  // 16j + r of the word shifted right by 4g.
+  auto make_sel_words = [&](const uint64_t (&mw)[2], bool (&sel)[2][4][4]) {
+    bool any = false;
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const uint64_t w = mw[qt] >> (4 * g);
+      const uint32_t half[2] = {static_cast<uint32_t>(w), static_cast<uint32_t>(w >> 32)};
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          sel[qt][j][r] = (half[j >> 1] & (1u << (16 * (j & 1) + r))) != 0u;
+          any |= sel[qt][j][r];
+        }
+    }
+    return __ballot(any) != 0;
+  };
+
   // Everything one wave does with key tile kt, staged in (kl, vl).
   auto compute = [&](const bool (&sel)[2][4][4], const DSA_LDS uint8_t* kl,
-                     const DSA_LDS uint8_t* vl) {
+                     const DSA_LDS uint8_t* vl) __attribute__((always_inline)) {
     // S^T = K . Q^T; A fragment = K row 16j+c16, chunk 4ks+g (swizzled):
     // byte offset kofs[ks] + 16j rows (swz_k(16j+c16) = swz_k(c16)).
+    // The K fragments of two 16-key tiles are read together before their
+    // products (a scheduling fence keeps them together), so one LDS latency
+    // is paid per half tile instead of one per fragment.
     f32x4 st[4][2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int jp = 0; jp < 4; jp += KJ) {
+      u32x4 ka[KJ][NKS];
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) st[j][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int jj = 0; jj < KJ; ++jj)
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        const u32x4 ka = *reinterpret_cast<const DSA_LDS u32x4*>(kl + kofs[ks] + 16 * j * (2 * D));
+        for (int ks = 0; ks < NKS; ++ks)
+          ka[jj][ks] = *reinterpret_cast<const DSA_LDS u32x4*>(kl + kofs[ks] + 16 * (jp + jj) * (2 * D));
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) st[j][qt] = M::run(ka, qf[qt][ks], st[j][qt]);
+      for (int jj = 0; jj < KJ; ++jj) {
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) st[jp + jj][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+          for (int qt = 0; qt < 2; ++qt)
+            st[jp + jj][qt] = M::run(ka[jj][ks], qf[qt][ks], st[jp + jj][qt]);
       }
     }
 
@@ -357,46 +487,83 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
     // O^T += V^T . P^T.  Lane (g, j=c16) addresses V row key0 + 4g + j/4,
     // dims 16dt + 4(j%4) .. +3; rows key0 + 16 and + 32 keep the swizzle, so
     // byte offset vofs[dt] + (32jj + 16h) rows.
+    // The V fragments of VG output tiles are read together before their
+    // products (one LDS latency per group, as for K above).
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
+    for (int dg = 0; dg < NDT; dg += VG) {
+      u32x4 vfrag[VG][2];
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const DSA_LDS uint8_t* va = vl + vofs[dt] + 32 * jj * (2 * D);
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((DSA_LDS s16x4*)va);
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((DSA_LDS s16x4*)(va + 16 * (2 * D)));
-        const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
-        const u32x4 vfrag = u32x4{l2.x, l2.y, h2.x, h2.y};
+      for (int d = 0; d < VG; ++d)
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) o[dt][qt] = M::run(vfrag, pf[qt][jj], o[dt][qt]);
-      }
+        for (int jj = 0; jj < 2; ++jj) {
+          const DSA_LDS uint8_t* va = vl + vofs[dg + d] + 32 * jj * (2 * D);
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((DSA_LDS s16x4*)va);
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((DSA_LDS s16x4*)(va + 16 * (2 * D)));
+          const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+          vfrag[d][jj] = u32x4{l2.x, l2.y, h2.x, h2.y};
+        }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int d = 0; d < VG; ++d)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+          for (int qt = 0; qt < 2; ++qt) o[dg + d][qt] = M::run(vfrag[d][jj], pf[qt][jj], o[dg + d][qt]);
     }
   };
 
-  // Per tile: scores -> mask (waits for the score loads), then the next
-  // tile's DMA is issued (so nothing below waits for it), then the products.
-  wait_dma_and_sync();
+  // Per tile kt (in buffers kt % 2, its scores already in sv): mask, then
+  // the DMA of tile kt+1 and the loads of its scores (in that order: the
+  // barrier at the end waits for the DMA only, vmcnt(NSL), and the score
+  // loads stay in flight across it), then the products.  Tiles below the
+  // block's first query (2 * tile of them, an even count) take the interior
+  // mask (no causal test); the one or two tiles on the diagonal the general
+  // one.
+  constexpr int NSL = MASK ? 2 : (VEC ? 8 : 32);  // selection load instructions per tile
   float sv[2][4][4];
+  uint64_t mw[2];
   bool sel[2][4][4];
-  for (int kt = 0; kt < nkt; kt += 2) {
-    // tile kt in buffers 0 (DMA'd before the barrier above); tile kt+1 -> buffers 1
-    load_scores(kt, sv);
-    bool act = make_sel(kt, sv, sel);
-    if (kt + 1 < nkt) {
-      dma_tile<D, true>(Kb, rowE, (kt + 1) * kKT, T, kb[1], wave, lane);
-      dma_tile<D, false>(Vb, rowE, (kt + 1) * kKT, T, vb[1], wave, lane);
+  auto load_sel = [&](int kt) __attribute__((always_inline)) {
+    if constexpr (MASK) load_words(kt, mw);
+    else load_scores(kt, sv);
+  };
+  auto step = [&](auto interior, int kt, DSA_LDS uint8_t* kc, DSA_LDS uint8_t* vc,
+                  DSA_LDS uint8_t* kn, DSA_LDS uint8_t* vn) __attribute__((always_inline)) {
+    bool act;
+    if constexpr (MASK) act = make_sel_words(mw, sel);
+    else act = decltype(interior)::value ? make_sel_fast(sv, sel) : make_sel(kt, sv, sel);
+    const bool more = kt + 1 < nkt;
+    if (more) {
+      const int s1 = (kt + 1) * kKT;
+      dma_tile<PW>(tile_rsrc(kbase, s1, T, rowbytes), koff, kn, wave);
+      dma_tile<PW>(tile_rsrc(vbase, s1, T, rowbytes), voff, vn, wave);
+      __builtin_amdgcn_sched_barrier(0);  // the DMA is issued before the selection loads
+      load_sel(kt + 1);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (act) compute(sel, kb[0], vb[0]);
-    wait_dma_and_sync();
-    if (kt + 1 >= nkt) break;
-    load_scores(kt + 1, sv);
-    act = make_sel(kt + 1, sv, sel);
-    if (kt + 2 < nkt) {
-      dma_tile<D, true>(Kb, rowE, (kt + 2) * kKT, T, kb[0], wave, lane);
-      dma_tile<D, false>(Vb, rowE, (kt + 2) * kKT, T, vb[0], wave, lane);
-    }
-    if (act) compute(sel, kb[1], vb[1]);
-    wait_dma_and_sync();
+    if (act) compute(sel, kc, vc);
+    if (more) wait_dma_keep<NSL>();
+    else wait_dma_keep<0>();
+    block_sync_lds();
+  };
+  using Interior = std::integral_constant<bool, true>;
+  using Diagonal = std::integral_constant<bool, false>;
+  DSA_LDS uint8_t* const kl0 = (DSA_LDS uint8_t*)k0;
+  DSA_LDS uint8_t* const kl1 = (DSA_LDS uint8_t*)k1;
+  DSA_LDS uint8_t* const vl0 = (DSA_LDS uint8_t*)v0;
+  DSA_LDS uint8_t* const vl1 = (DSA_LDS uint8_t*)v1;
+  __builtin_amdgcn_sched_barrier(0);
+  load_sel(0);
+  __builtin_amdgcn_sched_barrier(0);
+  wait_dma_keep<NSL>();
+  block_sync_lds();
+  const int nint = 2 * tile;  // < nkt: the block's first query t0 < T
+  for (int kt = 0; kt < nint; kt += 2) {
+    step(Interior{}, kt, kl0, vl0, kl1, vl1);
+    step(Interior{}, kt + 1, kl1, vl1, kl0, vl0);
   }
+  step(Diagonal{}, nint, kl0, vl0, kl1, vl1);
+  if (nint + 1 < nkt) step(Diagonal{}, nint + 1, kl1, vl1, kl0, vl0);
 
   // O = O^T / l, lane l: query tq[qt], dims 16dt + 4g .. +3.
 #pragma unroll
@@ -415,15 +582,68 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
 }
 
 template <typename Tag, int D>
-hipError_t launch(const TileArgs& a, hipStream_t stream) {
-  const int64_t nblk = a.B * a.HQ * ((a.T + kTQ - 1) / kTQ);
-  if (a.vec)
-    hipLaunchKernelGGL((tile_attn_kernel<Tag, D, true>), dim3(static_cast<unsigned>(nblk)),
-                       dim3(kNT), 0, stream, a);
+hipError_t launch(const TileArgs& a, int src, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(a.B * a.HQ * ((a.T + kTQ - 1) / kTQ)));
+  if (src == kSrcMask)
+    hipLaunchKernelGGL((tile_attn_kernel<Tag, D, kSrcMask>), grid, dim3(kNT), 0, stream, a);
+  else if (src == kSrcScores4)
+    hipLaunchKernelGGL((tile_attn_kernel<Tag, D, kSrcScores4>), grid, dim3(kNT), 0, stream, a);
   else
-    hipLaunchKernelGGL((tile_attn_kernel<Tag, D, false>), dim3(static_cast<unsigned>(nblk)),
-                       dim3(kNT), 0, stream, a);
+    hipLaunchKernelGGL((tile_attn_kernel<Tag, D, kSrcScores1>), grid, dim3(kNT), 0, stream, a);
   return hipGetLastError();
+}
+
+hipError_t launch_any(const TileArgs& a, int dtype, int D, int src, hipStream_t stream) {
+  if (dtype == 1) {
+    if (D == 64) return launch<BF16, 64>(a, src, stream);
+    if (D == 128) return launch<BF16, 128>(a, src, stream);
+  } else if (dtype == 2) {
+    if (D == 64) return launch<F16, 64>(a, src, stream);
+    if (D == 128) return launch<F16, 128>(a, src, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+// Selection bitmask of rows (b, t): word w holds keys 64w .. 64w+63, bit i
+// set iff key 64w + i <= t and scores[b,t,64w+i] >= thr[b*T+t] (a NaN score
+// or threshold selects nothing).  Words 0 .. min(W-1, (t|127)/64) of each
+// row are written, W = ceil(T/64): every word the tile kernel's block of
+// row t reads.  One wave per row, rows longest first; lane i tests key
+// 64w + i and the wave's ballot is word w.  Lane u keeps word 64c + u of
+// each group c of 64 words, so each group is one coalesced 512-byte store.
+__global__ __launch_bounds__(256) void selection_mask_kernel(const float* __restrict__ scores,
+                                                             int64_t ld,
+                                                             const float* __restrict__ thr,
+                                                             int64_t B, int T, int64_t ldm,
+                                                             uint64_t* __restrict__ mask) {
+  const int lane = lane_id();
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (idx >= B * T) return;  // whole waves
+  const int64_t b = idx % B;
+  const int t = T - 1 - static_cast<int>(idx / B);
+  const int64_t row = b * T + t;
+  const float th = thr[row];
+  const float* __restrict__ srow = scores + row * ld;
+  uint64_t* __restrict__ mrow = mask + row * ldm;
+  const int W = (T + 63) / 64;
+  const int nw = min(W, ((t | 127) >> 6) + 1);
+  constexpr int U = 16;  // loads in flight per lane
+  for (int c = 0; c < nw; c += 64) {
+    const int nu = min(64, nw - c);
+    uint64_t mine = 0;
+    for (int u = 0; u < nu; u += U) {
+      float v[U];
+#pragma unroll
+      for (int e = 0; e < U; ++e)  // in the row; read once: nontemporal
+        v[e] = __builtin_nontemporal_load(srow + min(64 * (c + u + e) + lane, t));
+#pragma unroll
+      for (int e = 0; e < U; ++e) {
+        const uint64_t bits = __ballot(64 * (c + u + e) + lane <= t && v[e] >= th);
+        mine = (lane == u + e) ? bits : mine;
+      }
+    }
+    if (lane < nu) mrow[c + lane] = mine;
+  }
 }
 
 }  // namespace
@@ -443,16 +663,27 @@ hipError_t launch_tile_attn(const float* scores, int64_t ld, const float* thr, c
                             int D, float scale, float* out, hipStream_t stream) {
   if (B == 0 || T == 0) return hipSuccess;
   const bool vec = (ld % 4 == 0) && ((reinterpret_cast<uintptr_t>(scores) & 15u) == 0);
-  TileArgs a{scores, ld, thr, Q, K, V, B, static_cast<int>(T), HQ,
-             scale * 1.4426950408889634f, out, vec ? 1 : 0};
-  if (dtype == 1) {
-    if (D == 64) return launch<BF16, 64>(a, stream);
-    if (D == 128) return launch<BF16, 128>(a, stream);
-  } else if (dtype == 2) {
-    if (D == 64) return launch<F16, 64>(a, stream);
-    if (D == 128) return launch<F16, 128>(a, stream);
-  }
-  return hipErrorInvalidValue;
+  const TileArgs a{scores, ld, thr, Q, K, V, B, static_cast<int>(T), HQ,
+                   scale * 1.4426950408889634f, out, nullptr, 0};
+  return launch_any(a, dtype, D, vec ? kSrcScores4 : kSrcScores1, stream);
+}
+
+hipError_t launch_tile_attn_mask(const uint64_t* mask, int64_t ldm, const void* Q, const void* K,
+                                 const void* V, int dtype, int64_t B, int64_t T, int HQ, int D,
+                                 float scale, float* out, hipStream_t stream) {
+  if (B == 0 || T == 0) return hipSuccess;
+  const TileArgs a{nullptr, 0, nullptr, Q, K, V, B, static_cast<int>(T), HQ,
+                   scale * 1.4426950408889634f, out, mask, ldm};
+  return launch_any(a, dtype, D, kSrcMask, stream);
+}
+
+hipError_t launch_selection_mask(const float* scores, int64_t ld, const float* thr, int64_t B,
+                                 int64_t T, uint64_t* mask, int64_t ldm, hipStream_t stream) {
+  if (B == 0 || T == 0) return hipSuccess;
+  const int64_t rows = B * T;
+  hipLaunchKernelGGL(selection_mask_kernel, dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256),
+                     0, stream, scores, ld, thr, B, static_cast<int>(T), ldm, mask);
+  return hipGetLastError();
 }
 
 }  // namespace dsa

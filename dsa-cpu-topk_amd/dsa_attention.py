@@ -82,9 +82,13 @@ def sparse_attention_hip(scores: torch.Tensor, threshold: torch.Tensor, Q, K, V,
 
     The library picks the kernel: per-query gathers; dense-masked MFMA tiles
     for T >= 4096 with 16-bit Q/K/V and DQ = DV in {64, 128}; K/V staged
-    through LDS for other long rows it covers (T >= 3072).
-    kernel="tiled" (or tiled=True) / "staged" runs that kernel at any T
-    (AssertionError for shapes it does not cover)."""
+    through LDS for other long rows it covers (T >= 3072).  Where it would
+    take the tiles, the selection is first reduced to a bitmask
+    (dsa_selection_mask, 1 bit per (query, key) instead of a 4-byte score
+    read once per head) and the tile kernel reads that (dsa_sparse_attn_mask):
+    the same output, bit for bit.
+    kernel="tiled" (or tiled=True) / "staged" / "mask" runs that kernel at
+    any T (AssertionError for shapes it does not cover)."""
     L.require_gpu(scores, threshold, Q, K, V)
     B, T, _ = scores.shape
     HQ, DQ = Q.shape[-2], Q.shape[-1]
@@ -99,6 +103,10 @@ def sparse_attention_hip(scores: torch.Tensor, threshold: torch.Tensor, Q, K, V,
         out = torch.empty(B, T, HQ, DV, device=Q.device, dtype=torch.float32)
     if tiled:
         kernel = "tiled"
+    if kernel is None and L.lib().dsa_sparse_attn_uses_mask(L.dtype_code(dt), T, HQ, DQ, DV):
+        kernel = "mask"
+    if kernel == "mask":
+        return _sparse_attention_mask(scores, thr, Q, K, V, dt, out)
     fn = {None: L.lib().dsa_sparse_attn_threshold,
           "tiled": L.lib().dsa_sparse_attn_threshold_tiled,
           "staged": L.lib().dsa_sparse_attn_threshold_staged}[kernel]
@@ -106,6 +114,35 @@ def sparse_attention_hip(scores: torch.Tensor, threshold: torch.Tensor, Q, K, V,
         scores.data_ptr(), T, thr.data_ptr(), Q.data_ptr(), K.data_ptr(), V.data_ptr(),
         L.dtype_code(dt), B, T, HQ, DQ, DV, 1.0 / math.sqrt(DQ), out.data_ptr(),
         L.stream_ptr(Q.device))
+    L.check(rc, "sparse_attention")
+    return out
+
+
+def selection_mask(scores: torch.Tensor, threshold: torch.Tensor) -> torch.Tensor:
+    """Bitmask of the causal threshold selection: int64 [B, T, ceil(T/64)],
+    bit i of word w of row (b, t) set iff 64w + i <= t and
+    scores[b, t, 64w + i] >= threshold[b, t] (words past a row's causal
+    range up to its 128-query block are 0, later ones are not written)."""
+    L.require_gpu(scores, threshold)
+    B, T, _ = scores.shape
+    assert threshold.numel() == B * T, "threshold must hold one value per query"
+    scores = L.prep(scores, torch.float32)
+    thr = L.prep(threshold, torch.float32)
+    W = (T + 63) // 64
+    mask = torch.empty(B, T, W, device=scores.device, dtype=torch.int64)
+    rc = L.lib().dsa_selection_mask(scores.data_ptr(), T, thr.data_ptr(), B, T, mask.data_ptr(), W,
+                                    L.stream_ptr(scores.device))
+    L.check(rc, "selection_mask")
+    return mask
+
+
+def _sparse_attention_mask(scores, thr, Q, K, V, dt, out):
+    B, T, HQ, DQ = Q.shape
+    DV = V.shape[-1]
+    mask = selection_mask(scores, thr)
+    rc = L.lib().dsa_sparse_attn_mask(
+        mask.data_ptr(), mask.shape[-1], Q.data_ptr(), K.data_ptr(), V.data_ptr(), L.dtype_code(dt),
+        B, T, HQ, DQ, DV, 1.0 / math.sqrt(DQ), out.data_ptr(), L.stream_ptr(Q.device))
     L.check(rc, "sparse_attention")
     return out
 

@@ -197,6 +197,47 @@ int dsa_sparse_attn_threshold_staged(const float* scores, int64_t ld, const floa
                                      int DV, float scale, float* out, void* stream);
 
 /*
+ * Selection bitmask of the threshold selection, for dsa_sparse_attn_mask.
+ * Row (b, t) of `mask` (ldm 64-bit words per row, ldm >= ceil(T/64)):
+ * bit i of word w is set iff key s = 64w + i has s <= t and
+ * scores[b,t,s] >= thr[b*T+t] (NaN scores or thresholds select nothing) --
+ * the selection dsa_sparse_attn_threshold applies.  Words 0 ..
+ * min(ceil(T/64)-1, (t|127)/64) of each row are written (those past the
+ * causal range are 0): every word dsa_sparse_attn_mask reads for that row.
+ * Replaces: the `scores >= thr` mask of _sparse_attn_kernel,
+ *           reference dsa_attention.py:265-290, computed once per (t, s)
+ *           instead of once per (t, s, head) -- no reference counterpart as
+ *           a separate call.
+ * Constraints: ld >= T; mask 8-byte aligned.
+ */
+int dsa_selection_mask(const float* scores, int64_t ld, const float* thr, int64_t B,
+                       int64_t T, uint64_t* mask, int64_t ldm, void* stream);
+
+/*
+ * Sparse attention with the selection read from a dsa_selection_mask
+ * bitmask: the dense-masked MFMA tile kernel, which reads 1 bit per
+ * (query, key) instead of a 4-byte score (per head).  Together with
+ * dsa_selection_mask the same result, bit for bit, as the tile kernel of
+ * dsa_sparse_attn_threshold / dsa_sparse_attn_threshold_tiled on the same
+ * scores and thresholds.
+ * Replaces: _sparse_attn_kernel + sparse_attention_with_threshold_triton
+ *           (reference dsa_attention.py:234-324) where it runs on tiles.
+ * Constraints: bf16/fp16; DQ = DV in {64, 128}; ldm >= ceil(T/64),
+ *   ldm < 2^21; T*HQ*D*2 < 4 GiB; Q, K, V, out 16-byte aligned, mask
+ *   8-byte aligned.  Other shapes return DSA_EUNSUPPORTED.
+ */
+int dsa_sparse_attn_mask(const uint64_t* mask, int64_t ldm, const void* Q, const void* K,
+                         const void* V, int dtype, int64_t B, int64_t T, int HQ, int DQ,
+                         int DV, float scale, float* out, void* stream);
+
+/*
+ * 1 if dsa_sparse_attn_threshold runs this shape on the tile kernel (so
+ * dsa_selection_mask + dsa_sparse_attn_mask apply and give its result),
+ * else 0.  Pure function of the arguments.
+ */
+int dsa_sparse_attn_uses_mask(int dtype, int64_t T, int HQ, int DQ, int DV);
+
+/*
  * Fused DSA forward for T <= 2048: indexer -> per-row radix select ->
  * sparse attention in one kernel; the score rows live in LDS only.
  * Same result as dsa_indexer_scores + dsa_topk_threshold(k = min(top_k,T),

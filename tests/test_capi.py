@@ -4,6 +4,7 @@ keeps the reference's error classes.  No kernel is launched here."""
 from __future__ import annotations
 
 import ctypes
+import math
 import os
 import re
 
@@ -211,6 +212,50 @@ def test_tiled_rejects_rows_past_4gib():
     # just under the bound is accepted (B = 0: nothing launched)
     assert f(FAKE, T, FAKE, FAKE, FAKE, FAKE, L.DSA_BF16, 0, T, 8, 128, 128, 0.1, FAKE,
              None) == L.DSA_OK
+
+
+def test_selection_mask_and_mask_attention_checks():
+    """Bitmask entry points: row width, dtype/shape coverage and the 32-bit
+    mask-row offsets are checked before any HIP call; B = 0 launches
+    nothing."""
+    sm = L.lib().dsa_selection_mask
+    assert _rc(sm, FAKE, 300, FAKE, 2, 300, FAKE, 4, None)[0] == L.DSA_EINVAL     # ldm < 5
+    assert _rc(sm, FAKE, 299, FAKE, 2, 300, FAKE, 5, None)[0] == L.DSA_EINVAL     # ld < T
+    assert _rc(sm, None, 300, FAKE, 2, 300, FAKE, 5, None)[0] == L.DSA_EINVAL     # null
+    assert _rc(sm, FAKE, 300, FAKE, 2, 300, FAKE + 4, 5, None)[0] == L.DSA_EINVAL  # misaligned
+    assert sm(FAKE, 300, FAKE, 0, 300, FAKE, 5, None) == L.DSA_OK
+    am = L.lib().dsa_sparse_attn_mask
+    ok = [FAKE, 5, FAKE, FAKE, FAKE, L.DSA_BF16, 1, 300, 4, 64, 64, 0.125, FAKE, None]
+
+    def call(**kw):
+        a = list(ok)
+        for k, v in kw.items():
+            a[int(k[1:])] = v
+        return _rc(am, *a)
+
+    assert call(a5=L.DSA_F32)[0] == L.DSA_EUNSUPPORTED        # fp32
+    assert call(a9=32, a10=32)[0] == L.DSA_EUNSUPPORTED       # D = 32
+    assert call(a9=64, a10=128)[0] == L.DSA_EUNSUPPORTED      # DQ != DV
+    assert call(a1=4)[0] == L.DSA_EINVAL                      # ldm < ceil(T/64)
+    assert call(a1=1 << 21)[0] == L.DSA_EINVAL                # mask rows past 32-bit offsets
+    assert call(a0=FAKE + 4)[0] == L.DSA_EINVAL               # mask misaligned
+    assert call(a11=math.inf)[0] == L.DSA_EINVAL              # scale
+    assert call(a6=0)[0] == L.DSA_OK                          # B = 0
+
+
+def test_mask_path_rule():
+    """dsa_sparse_attn_uses_mask: the shapes dsa_sparse_attn_threshold runs on
+    the tile kernel (16-bit, DQ = DV in {64, 128}; T >= 4096 or heads too
+    wide to gather)."""
+    u = L.lib().dsa_sparse_attn_uses_mask
+    assert u(L.DSA_BF16, 16384, 16, 128, 128) == 1
+    assert u(L.DSA_F16, 4096, 4, 64, 64) == 1
+    assert u(L.DSA_BF16, 4095, 4, 64, 64) == 0
+    assert u(L.DSA_BF16, 512, 128, 128, 128) == 1        # 16 K wide rows: tiles at any T
+    assert u(L.DSA_F32, 16384, 16, 128, 128) == 0
+    assert u(L.DSA_BF16, 16384, 16, 64, 128) == 0
+    assert u(L.DSA_BF16, 16384, 16, 32, 32) == 0
+    assert u(99, 16384, 16, 128, 128) == 0
 
 
 def test_fused_rejects_bad_arguments():

@@ -170,6 +170,101 @@ def test_tiled_unsupported_shapes_raise(dev):
                              tiled=True)
 
 
+# --- selection bitmask + the tile kernel reading it ------------------------
+def _mask_bits_oracle(scores, thr):
+    """The bitmask dsa_selection_mask must write, from the selection rule
+    itself (per key: s <= t and score >= thr), packed with numpy."""
+    import numpy as np
+    B, T, _ = scores.shape
+    W = (T + 63) // 64
+    s = np.arange(W * 64)
+    sc = np.full((B, T, W * 64), np.nan, dtype=np.float32)
+    sc[:, :, :T] = scores.numpy()
+    sel = (s[None, None, :] <= np.arange(T)[None, :, None]) & (sc >= thr.reshape(B, T, 1).numpy())
+    bits = sel.reshape(B, T, W, 64).astype(np.uint64) << np.arange(64, dtype=np.uint64)
+    return bits.sum(axis=-1, dtype=np.uint64)
+
+
+@pytest.mark.parametrize("B,T", [(1, 64), (2, 130), (1, 300), (3, 257), (1, 1000)])
+def test_selection_mask_bits(dev, B, T):
+    """Every word a row's 128-query block reads, bit for bit, against the
+    selection rule applied key by key: ties at the threshold, NaN scores,
+    +-inf scores, a NaN and an +inf threshold, ragged T."""
+    from dsa_attention import selection_mask
+
+    say(f"selection mask B={B} T={T}")
+    g = torch.Generator().manual_seed(T)
+    s = torch.randn(B, T, T, generator=g)
+    s = torch.where(torch.rand(B, T, T, generator=g) < 0.1, 0.0, s)
+    s[0, :, 3] = math.nan
+    s[0, :, 5] = math.inf
+    s[-1, :, 7 % T] = -math.inf
+    thr = kth(16)(s)
+    thr[0, T // 2, 0] = math.nan
+    thr[-1, T - 1, 0] = math.inf
+    got = selection_mask(s.to(dev), thr.to(dev)).cpu().numpy().view("uint64")
+    want = _mask_bits_oracle(s, thr)
+    W = (T + 63) // 64
+    for t in range(T):
+        nw = min(W, (t | 127) // 64 + 1)
+        assert (got[:, t, :nw] == want[:, t, :nw]).all(), f"row {t}"
+
+
+@pytest.mark.parametrize("B,T,HQ,D,k,dtype", [(1, 128, 4, 64, 8, BF), (2, 300, 2, 128, 40, BF),
+                                              (1, 257, 1, 64, 16, HF), (2, 200, 16, 128, 20, BF),
+                                              (1, 1000, 3, 64, 100, HF), (1, 129, 2, 128, 200, BF)])
+def test_mask_kernel_equals_tiled(dev, B, T, HQ, D, k, dtype):
+    """The bitmask path (dsa_selection_mask + dsa_sparse_attn_mask) gives the
+    scores-reading tile kernel's output bit for bit, and the oracle's within
+    the 16-bit tolerance."""
+    out = run_case(dev, B, T, HQ, D, D, kth(k), dtype=dtype, rtol=2e-2, atol=2e-2, kernel="mask")
+    _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, HQ, D, D, dtype=dtype, seed0=0)
+    g = torch.Generator().manual_seed(17)
+    scores = torch.randn(B, T, T, generator=g)
+    scores = torch.where(torch.rand(B, T, T, generator=g) < 0.1, 0.0, scores)
+    ref = sparse_attention_hip(scores.to(dev), kth(k)(scores).to(dev), Q.to(dev), K.to(dev),
+                               V.to(dev), kernel="tiled")
+    assert torch.equal(out, ref)
+
+
+def test_mask_kernel_empty_rows_and_dense(dev):
+    """NaN / +inf thresholds give NaN rows; -inf selects every causal key."""
+    B, T, HQ, D = 1, 300, 2, 64
+    _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, HQ, D, D, dtype=BF)
+    s = torch.randn(B, T, T, generator=torch.Generator().manual_seed(5))
+    thr = kth(16)(s)
+    bad = torch.tensor([0, 7, 130, 299])
+    thr[0, bad[:2], 0] = math.inf
+    thr[0, bad[2:], 0] = math.nan
+    args = (Q.to(dev), K.to(dev), V.to(dev))
+    out = sparse_attention_hip(s.to(dev), thr.to(dev), *args, kernel="mask").cpu()
+    assert bool(torch.isnan(out[0, bad]).all())
+    good = torch.ones(T, dtype=torch.bool)
+    good[bad] = False
+    want = O.sparse_attn_threshold(s, thr, Q, K, V)
+    assert close(out[0, good], want[0, good], 2e-2, 2e-2)[0]
+    dense = torch.full((B, T, 1), -math.inf)
+    out = sparse_attention_hip(s.to(dev), dense.to(dev), *args, kernel="mask").cpu()
+    assert close(out, O.sparse_attn_threshold(s, dense, Q, K, V), 2e-2, 2e-2)[0]
+
+
+def test_mask_path_is_the_default_for_tile_shapes(dev):
+    """At T >= 4096 (16-bit, D = 128) the wrapper takes the bitmask path; its
+    output equals the scores-reading tile kernel's bit for bit."""
+    B, T, HQ, D = 1, 4096, 2, 128
+    _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, HQ, D, D, dtype=BF)
+    s = torch.randn(B, T, T, generator=torch.Generator().manual_seed(3)).to(dev)
+    sd = s.masked_fill(~torch.ones(T, T, dtype=torch.bool, device=dev).tril(), -math.inf)
+    thr = torch.topk(sd, 256, dim=-1).values[..., -1:].contiguous()
+    args = (s, thr, Q.to(dev), K.to(dev), V.to(dev))
+    a = sparse_attention_hip(*args)
+    b = sparse_attention_hip(*args, kernel="tiled")
+    assert torch.equal(a, b)
+    rows = [0, 1, 63, 64, 127, 128, 2047, 4095]
+    want = O.sparse_attn_threshold(s.cpu()[:, rows], thr.cpu()[:, rows], Q, K, V, rows=rows)
+    assert close(a.cpu()[:, rows], want, 2e-2, 2e-2)[0]
+
+
 # ---------------------------------------------------------------------------
 # Wide attention rows.  The reference only asserts powers of two
 # (dsa_attention.py:298-304); rows wider than one wave's registers (fp32
