@@ -13,10 +13,19 @@
 // Block = 4 waves = 128 consecutive queries of one (batch element, head);
 // wave w owns queries t0+32w .. t0+32w+31 (two 16-query MFMA column tiles).
 // Key tiles of 64 keys are copied HBM -> LDS by the DMA path
-// (global_load_lds_dwordx4: no registers, no LDS store instructions), K and
-// V both as plain [key][d] rows, double-buffered with one barrier per tile.
-// Rows are stored with their 16-byte chunks XOR-swizzled by row so that
-// every LDS read pattern below hits distinct banks.
+// (buffer_load_dwordx4 ... lds: no registers, no LDS store instructions;
+// range-checked, so rows past T read as zeros), K and V both as plain
+// [key][d] rows, double-buffered with one barrier per tile.  Rows are
+// stored with their 16-byte chunks XOR-swizzled by row so that every LDS
+// read pattern below hits distinct banks.
+//
+// The selection of a wave's 32 x 64 tile comes either from the fp32 score
+// rows and thresholds (kSrcScores*: 8 KB per wave and tile, read by every
+// head's block) or from a bitmask built once per (query, key) by
+// selection_mask_kernel (kSrcMask: 256 bytes per wave and tile; config 4:
+// 1.47 -> 1.10 ms for the kernel, 1.37 GB instead of 7.5 GB of L2 misses).
+// Either is loaded one tile ahead, behind the next tile's DMA, and the
+// barrier waits for the DMA only.
 //
 // The products are computed transposed, so that no lane exchanges are needed
 // between them (16x16x32 MFMA: A[m][k] lane l holds m = l%16, k-slots
@@ -46,12 +55,12 @@
 #include "dsa_launch.h"
 
 typedef float dsa_f32x4 __attribute__((ext_vector_type(4)));
-// Raw buffer loads of fp32 data, declared outside any namespace so that
-// the asm labels bind the intrinsics (the LLVM intrinsics, typed as float: the
-// integer-vector forms of the clang builtins are narrowed to one dword by
-// this toolchain's optimiser, which then repeats that dword in every
-// element).  Arguments: resource, byte offset (VGPR), SGPR offset, cache
-// policy.
+// Raw buffer loads (the LLVM intrinsics, bound by asm label, so declared
+// outside any namespace).  They are typed as float on purpose: this
+// toolchain's optimiser narrows the integer-vector forms (and the clang
+// builtin __builtin_amdgcn_raw_buffer_load_b128) to a single dword and
+// repeats it in every element.  Arguments: resource, byte offset (VGPR),
+// SGPR offset, cache policy.
 __device__ dsa_f32x4 buffer_load_f32x4(__amdgpu_buffer_rsrc_t rsrc, int voffset, int soffset, int aux)
     __asm("llvm.amdgcn.raw.ptr.buffer.load.v4f32");
 __device__ float buffer_load_f32(__amdgpu_buffer_rsrc_t rsrc, int voffset, int soffset, int aux)
