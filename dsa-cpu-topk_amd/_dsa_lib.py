@@ -54,6 +54,8 @@ _SIGNATURES = {
     "dsa_selection_mask": ([_P, _I64, _P, _I64, _I64, _P, _I64, _P], _I),
     "dsa_sparse_attn_mask": ([_P, _I64, _P, _P, _P, _I, _I64, _I64, _I, _I, _I, _F, _P, _P], _I),
     "dsa_sparse_attn_uses_mask": ([_I, _I64, _I, _I, _I], _I),
+    "dsa_sparse_attn_mask_noalloc": ([_P, _I64, _P, _P, _P, _P, _I, _I64, _I64, _I, _I, _I, _F,
+                                      _P, _P], _I),
 }
 
 

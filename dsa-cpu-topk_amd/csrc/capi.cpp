@@ -241,6 +241,34 @@ int dsa_sparse_attn_mask(const uint64_t* mask, int64_t ldm, const void* Q, const
                     "dsa_sparse_attn_mask");
 }
 
+int dsa_sparse_attn_mask_noalloc(const float* scores, int64_t ld, const float* thr, const void* Q,
+                                 const void* K, const void* V, int dtype, int64_t B, int64_t T,
+                                 int HQ, int DQ, int DV, float scale, float* out, void* stream) {
+  if (!dtype_ok(dtype)) return fail(DSA_EINVAL, "sparse_attn_mask_noalloc: unknown dtype %d", dtype);
+  if (B < 0 || T < 0) return fail(DSA_EINVAL, "sparse_attn_mask_noalloc: negative size");
+  if (T > kMaxElems) return fail(DSA_EINVAL, "sparse_attn_mask_noalloc: T=%lld too large", (long long)T);
+  if (HQ < 1 || HQ > 1024) return fail(DSA_EINVAL, "sparse_attn_mask_noalloc: HQ=%d outside [1,1024]", HQ);
+  if (!std::isfinite(scale)) return fail(DSA_EINVAL, "sparse_attn_mask_noalloc: scale must be finite");
+  if (dtype == DSA_F32 || dtype == DSA_FP8 || DQ != DV || (DQ != 64 && DQ != 128))
+    return fail(DSA_EUNSUPPORTED, "sparse_attn_mask_noalloc: needs bf16/fp16 and DQ = DV in {64,128} (dtype %d DQ=%d DV=%d)", dtype, DQ, DV);
+  if (ld < T) return fail(DSA_EINVAL, "sparse_attn_mask_noalloc: ld=%lld < T=%lld", (long long)ld, (long long)T);
+  const int64_t words = B * T * ((T + 63) / 64);
+  if (words > dsa::kScratchWords)
+    return fail(DSA_EINVAL, "sparse_attn_mask_noalloc: the bitmask needs B*T*ceil(T/64) = %lld words, above the static scratch of %lld words (32 MiB); use dsa_selection_mask + dsa_sparse_attn_mask with a caller-allocated mask",
+                (long long)words, (long long)dsa::kScratchWords);
+  if (T * HQ * static_cast<int64_t>(DQ) * 2 > (int64_t{1} << 32) - 1)
+    return fail(DSA_EINVAL, "sparse_attn_mask_noalloc: T*HQ*D = %lld 16-bit elements must be < 4 GiB",
+                (long long)(T * HQ * static_cast<int64_t>(DQ)));
+  if (B * T == 0) return DSA_OK;
+  if (!scores || !thr || !Q || !K || !V || !out) return fail(DSA_EINVAL, "sparse_attn_mask_noalloc: null pointer");
+  if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(out))
+    return fail(DSA_EINVAL, "sparse_attn_mask_noalloc: Q/K/V/out must be 16-byte aligned");
+  return hip_status(dsa::launch_sparse_attn_mask_noalloc(scores, ld, thr, Q, K, V, dtype, B, T, HQ,
+                                                         DQ, scale, out,
+                                                         static_cast<hipStream_t>(stream)),
+                    "dsa_sparse_attn_mask_noalloc");
+}
+
 int dsa_sparse_attn_uses_mask(int dtype, int64_t T, int HQ, int DQ, int DV) {
   return dtype_ok(dtype) && dsa::sparse_attn_uses_tiles(dtype, T, HQ, DQ, DV) ? 1 : 0;
 }

@@ -58,6 +58,13 @@ hipError_t launch_tile_attn_mask(const uint64_t* mask, int64_t ldm, const void* 
                                  float scale, float* out, hipStream_t stream);
 hipError_t launch_selection_mask(const float* scores, int64_t ld, const float* thr, int64_t B,
                                  int64_t T, uint64_t* mask, int64_t ldm, hipStream_t stream);
+// The bitmask path with the bitmask in a static per-GPU array of
+// kScratchWords words (32 MiB: B*T*ceil(T/64) <= 2^22, e.g. B=1, T=16384).
+constexpr int64_t kScratchWords = int64_t{1} << 22;
+hipError_t launch_sparse_attn_mask_noalloc(const float* scores, int64_t ld, const float* thr,
+                                           const void* Q, const void* K, const void* V, int dtype,
+                                           int64_t B, int64_t T, int HQ, int D, float scale,
+                                           float* out, hipStream_t stream);
 
 // The same attention with each block's causal K/V rows staged through LDS
 // (staged_attn.hip): rows of 64*E elements, DQ = DV, E in {4, 8} for fp32

@@ -49,6 +49,7 @@
 // uses fp32 probabilities; the difference is far inside the 16-bit
 // tolerance); everything else is fp32.  Rows that select nothing get
 // 0/0 = NaN, as the reference.
+#include <mutex>
 #include <type_traits>
 
 #include "dsa_device.h"
@@ -684,6 +685,56 @@ hipError_t launch_tile_attn_mask(const uint64_t* mask, int64_t ldm, const void* 
   const TileArgs a{nullptr, 0, nullptr, Q, K, V, B, static_cast<int>(T), HQ,
                    scale * 1.4426950408889634f, out, mask, ldm};
   return launch_any(a, dtype, D, kSrcMask, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant of the bitmask path: the bitmask lives in this
+// file-scope device array (one copy per GPU, held until the process ends).
+// Host code never passes `scratch` itself to a kernel: its address on each
+// device comes from hipGetSymbolAddress, looked up once per device with
+// that device current, and that pointer is what the kernels get.
+// Calls on one GPU share the array: calls that overlap in time on one GPU
+// (different streams, different host threads) race.  Nothing in it needs
+// clearing: the mask kernel writes every word the attention kernel reads.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint64_t scratch[kScratchWords];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint64_t* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+hipError_t scratch_words(uint64_t** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (ptr == nullptr) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = static_cast<uint64_t*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+
+hipError_t launch_sparse_attn_mask_noalloc(const float* scores, int64_t ld, const float* thr,
+                                           const void* Q, const void* K, const void* V, int dtype,
+                                           int64_t B, int64_t T, int HQ, int D, float scale,
+                                           float* out, hipStream_t stream) {
+  if (B == 0 || T == 0) return hipSuccess;
+  const int64_t ldm = (T + 63) / 64;
+  if (B * T * ldm > kScratchWords) return hipErrorInvalidValue;  // the caller checked
+  uint64_t* mask = nullptr;
+  hipError_t e = scratch_words(&mask);
+  if (e != hipSuccess) return e;
+  e = launch_selection_mask(scores, ld, thr, B, T, mask, ldm, stream);
+  if (e != hipSuccess) return e;
+  return launch_tile_attn_mask(mask, ldm, Q, K, V, dtype, B, T, HQ, D, scale, out, stream);
 }
 
 hipError_t launch_selection_mask(const float* scores, int64_t ld, const float* thr, int64_t B,

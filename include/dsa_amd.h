@@ -231,6 +231,26 @@ int dsa_sparse_attn_mask(const uint64_t* mask, int64_t ldm, const void* Q, const
                          int DV, float scale, float* out, void* stream);
 
 /*
+ * dsa_selection_mask + dsa_sparse_attn_mask in one call that allocates
+ * nothing: the bitmask goes into a static device array of the library
+ * (32 MiB per GPU the library runs on, held until the process ends), so
+ * the caller passes only what dsa_sparse_attn_threshold takes.  Same output,
+ * bit for bit, as that pair (and as the tile kernel of
+ * dsa_sparse_attn_threshold_tiled).
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).
+ * Limit: B*T*ceil(T/64) <= 2^22 (B=1, T=16384 fits); larger inputs return
+ *   DSA_EINVAL.  Shapes: those of dsa_sparse_attn_mask (bf16/fp16,
+ *   DQ = DV in {64, 128}); ld >= T.  Calls that overlap in time on one GPU
+ *   share the array and race; the device is the current one.
+ */
+int dsa_sparse_attn_mask_noalloc(const float* scores, int64_t ld, const float* thr,
+                                 const void* Q, const void* K, const void* V, int dtype,
+                                 int64_t B, int64_t T, int HQ, int DQ, int DV, float scale,
+                                 float* out, void* stream);
+
+/*
  * 1 if dsa_sparse_attn_threshold runs this shape on the tile kernel (so
  * dsa_selection_mask + dsa_sparse_attn_mask apply and give its result),
  * else 0.  Pure function of the arguments.

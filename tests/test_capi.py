@@ -243,6 +243,28 @@ def test_selection_mask_and_mask_attention_checks():
     assert call(a6=0)[0] == L.DSA_OK                          # B = 0
 
 
+def test_noalloc_entry_checks():
+    """dsa_sparse_attn_mask_noalloc: inputs whose bitmask exceeds the static
+    scratch (B*T*ceil(T/64) > 2^22 words) and uncovered shapes are refused
+    before any HIP call; B = 0 launches nothing."""
+    f = L.lib().dsa_sparse_attn_mask_noalloc
+    T = 16384
+    ok = [FAKE, T, FAKE, FAKE, FAKE, FAKE, L.DSA_BF16, 1, T, 16, 128, 128, 0.1, FAKE, None]
+    a = list(ok)
+    a[7] = 2                                            # 2 x 16384 x 256 words
+    rc, msg = _rc(f, *a)
+    assert rc == L.DSA_EINVAL and "static scratch" in msg, (rc, msg)
+    a = list(ok)
+    a[6] = L.DSA_F32
+    assert _rc(f, *a)[0] == L.DSA_EUNSUPPORTED
+    a = list(ok)
+    a[1] = T - 1                                        # ld < T
+    assert _rc(f, *a)[0] == L.DSA_EINVAL
+    a = list(ok)
+    a[7] = 0
+    assert f(*a) == L.DSA_OK
+
+
 def test_mask_path_rule():
     """dsa_sparse_attn_uses_mask: the shapes dsa_sparse_attn_threshold runs on
     the tile kernel (16-bit, DQ = DV in {64, 128}; T >= 4096 or heads too
