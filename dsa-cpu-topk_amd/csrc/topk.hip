@@ -577,13 +577,29 @@ constexpr int kFinGather = 64;   // kept values of one finishing bin ranked in r
 // registers (a bin holding more than kFinGather, i.e. heavy ties, takes
 // radix passes over the kept keys).  A row of at most four chunks is its own
 // sample (delta = 0).
-template <int NT>
+//
+// IDX (rows of at most 16 chunks): the exactly-k index set too, from the
+// same single read of the row.  While streaming, each thread records which
+// of its entries lie above the interval (certainly selected: abv, bit 4j+c
+// for position (j*NT+tid)*4+c) and which it kept (kpt, in the order it
+// streamed them, the order of its kept values).  Once the threshold is
+// known, each thread sorts its kept values into above / equal to it; the
+// flags go to LDS bitmaps in position order, and one block-wide scan over
+// 64-position ranges places every selected entry at #(above before it) +
+// min(#(equal before it), k - #above), ascending positions -- emit_indices'
+// rule without a pass per chunk.
+template <int NT, bool IDX>
 __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
   constexpr int NW = NT / kWave;
   constexpr int CH = 4 * NT;  // entries per chunk (one float4 per thread)
   constexpr int CAP = 19;     // LDS column slots per thread
   static_assert(NT == 256 && kBrBins == 4 * NT, "layout below assumes 4 waves of 4 bins");
   static_assert(CAP * NT >= kCandCap + kFinBins + kFinGather, "finish fits the columns");
+  // IDX: the flag bitmap (16*NT bytes) sits past the finishing wave's LDS;
+  // k indices of up to kIdxStage are staged in the columns' LDS afterwards.
+  constexpr int kIdxMapWord = (kCandCap + kFinBins + kFinGather + 3) & ~3;
+  constexpr int kIdxStage = CAP * NT;
+  static_assert(!IDX || kIdxMapWord + 16 * NT / 4 <= CAP * NT, "the IDX bitmap fits the columns");
   // lds: sample histogram [0, kBrBins), then per-thread columns (slot s of
   // thread t at s*NT + t), then the compacted kept list [0, n_kept) with the
   // finishing wave's histogram and gather list at kCandCap.
@@ -592,6 +608,7 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
   __shared__ uint32_t info[6];
   __shared__ float wext[2 * NW];
   __shared__ uint32_t wcnt[NW], wbad[NW];
+  __shared__ float rsh[1];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -705,12 +722,26 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
   uint32_t below = 0, kc = 0;  // this thread: valid values below fhi; kept
   bool bad = false;            // wave-uniform: a column came near CAP
   uint32_t* col = lds + tid;
-  auto take = [&](float v, bool valid) {
+  uint64_t abv = 0, kpt = 0;   // IDX: entries above the interval; kept entries
+  // Returns bit 0: kept, bit 1: above the interval (NaN included).
+  auto take = [&](float v, bool valid) -> uint32_t {
     const bool lt = valid && v < fhi;
     const bool kp = lt && !(v < flo);
     col[kc * NT] = __float_as_uint(v);  // the next free slot; kept only if kc advances
     below += lt ? 1u : 0u;
     kc += kp ? 1u : 0u;
+    return (kp ? 1u : 0u) | ((valid && !lt) ? 2u : 0u);
+  };
+  // IDX: a chunk's 4 results into the masks (chunk j, streaming slot sl).
+  auto record = [&](uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3, int j, int sl) {
+    if constexpr (IDX) {
+      const uint32_t nk = (r0 & 1u) | ((r1 & 1u) << 1) | ((r2 & 1u) << 2) | ((r3 & 1u) << 3);
+      const uint32_t na = (r0 >> 1) | ((r1 >> 1) << 1) | ((r2 >> 1) << 2) | ((r3 >> 1) << 3);
+      abv |= static_cast<uint64_t>(na) << (4 * j);
+      kpt |= static_cast<uint64_t>(nk) << (4 * sl);
+    } else {
+      (void)r0; (void)r1; (void)r2; (void)r3; (void)j; (void)sl;
+    }
   };
   // Before every 4 values: a column with fewer than 4 free slots stops the
   // wave (the row then takes the exact passes).
@@ -721,21 +752,23 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     if (room()) {
+      uint32_t r[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) take(sv[4 * s + c], !whole || sample_in(4 * s + c));
+      for (int c = 0; c < 4; ++c) r[c] = take(sv[4 * s + c], !whole || sample_in(4 * s + c));
+      record(r[0], r[1], r[2], r[3], sample_chunk(s), s);
     }
   }
 
+  auto chunk_of = [&](int u) {  // u-th chunk that is not a sample chunk
+    int j = u;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) j += ((s * nc) / 4 <= j) ? 1 : 0;
+    return j;
+  };
   if (!whole && !bad) {
     // Chunks outside the sample, 4 per step, the next step's loads in flight
     // while this step's values are classified.
     const int ns = nc - 4;
-    auto chunk_of = [&](int u) {  // u-th chunk that is not a sample chunk
-      int j = u;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) j += ((s * nc) / 4 <= j) ? 1 : 0;
-      return j;
-    };
     const int nsteps = (ns + 3) / 4;
     float4 cur[4];
     int jc[4];
@@ -756,14 +789,16 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
       for (int q = 0; q < 4; ++q) {
         const float fv[4] = {cur[q].x, cur[q].y, cur[q].z, cur[q].w};
         if (4 * it + q < ns && room()) {  // else a repeated load past the last chunk
+          uint32_t r[4];
           if ((jc[q] + 1) * CH <= nv) {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) take(fv[c], true);
+            for (int c = 0; c < 4; ++c) r[c] = take(fv[c], true);
           } else {
             const int p0 = (jc[q] * NT + tid) * 4;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) take(fv[c], p0 + c < nv);
+            for (int c = 0; c < 4; ++c) r[c] = take(fv[c], p0 + c < nv);
           }
+          record(r[0], r[1], r[2], r[3], jc[q], 4 + 4 * it + q);
         }
       }
 #pragma unroll
@@ -802,91 +837,186 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
 #pragma unroll
     for (int s = 0; s < CAP; ++s)
       if (static_cast<uint32_t>(s) < kc) lds[kbase + s] = mine[s];
-    block_sync_lds();
-    if (wid != 0) return;
-    const uint32_t krem = ku - tot_above;
-    auto visit_kept = [&](auto&& f) {
-      for (uint32_t i = lane; i < ktot; i += kWave) f(__uint_as_float(lds[i]));
-    };
-    // Value bins over the kept values' own range (all below fhi, so NaN is
-    // never kept; -inf may be).
-    float khi = -__builtin_huge_valf(), klo = __builtin_huge_valf();
-    visit_kept([&](float v) {
-      khi = fmaxf(khi, v);
-      klo = fminf(klo, v);
-    });
-    khi = wave_extreme_f32<true>(khi);
-    klo = wave_extreme_f32<false>(klo);
-    const float krange = khi - klo;
-    const float ks = static_cast<float>(kFinBins) / krange;
-    // Bins need a finite range (klo > -inf); else all equal or -inf kept.
-    const bool binned = krange > 0.0f && krange <= __FLT_MAX__ && ks <= __FLT_MAX__;
-    uint32_t* fh = lds + kCandCap;
-    reinterpret_cast<uint4*>(fh)[lane] = make_uint4(0u, 0u, 0u, 0u);
-    wave_lds_sync();
-    if (binned) visit_kept([&](float v) { atomicAdd(&fh[value_bin(v, klo, ks, kFinBins - 1)], 1u); });
-    else if (lane == 0) fh[0] = ktot;  // one bin: the radix passes below
-    wave_lds_sync();
-    // Suffix scan over the bins (4 per lane) for the bin holding rank krem.
-    const uint4 h4 = reinterpret_cast<const uint4*>(fh)[lane];
-    const uint32_t h[4] = {h4.x, h4.y, h4.z, h4.w};
-    const uint32_t local = h[0] + h[1] + h[2] + h[3];
-    const uint32_t incl = wave_inclusive_sum(local);
-    const uint32_t abv = wave_read_lane(incl, kWave - 1) - incl;
-    const bool here = abv < krem && abv + local >= krem;
-    uint32_t bsel = 0, brank = 0, bcnt = 0;
-    if (here) {
-      uint32_t cum = abv;
+    // IDX: the row's flags as an LDS bitmap in position order, past what the
+    // finishing wave uses: byte j*NT+t holds positions (j*NT+t)*4 .. +3,
+    // above the threshold in the low nibble, equal to it in the high one.
+    // The values above the interval go in now, while wave 0 finishes.
+    uint8_t* fb = reinterpret_cast<uint8_t*>(lds + kIdxMapWord);
+    if constexpr (IDX) {
 #pragma unroll
-      for (int i = 3; i >= 0; --i) {
-        if (bcnt == 0u && cum + h[i] >= krem) {
-          bsel = 4u * lane + i;
-          brank = krem - cum;
-          bcnt = h[i];
-        }
-        cum += h[i];
-      }
+      for (int j = 0; j < 16; ++j) fb[j * NT + tid] = static_cast<uint8_t>((abv >> (4 * j)) & 15u);
     }
-    const int srcl = __ffsll(static_cast<unsigned long long>(ballot(here))) - 1;
-    bsel = wave_read_lane(bsel, srcl);
-    brank = wave_read_lane(brank, srcl);
-    bcnt = wave_read_lane(bcnt, srcl);
-    float res;
-    if (binned && bcnt <= static_cast<uint32_t>(kFinGather)) {
-      // Gather the chosen bin's values, then rank them against each other:
-      // the wanted one has fewer than brank greater and at least brank
-      // greater-or-equal.
-      uint32_t* gl = fh + kFinBins;
-      uint32_t ng = 0;
+    block_sync_lds();
+    if (wid == 0) {  // one wave finishes on the kept list
+      const uint32_t krem = ku - tot_above;
+      auto visit_kept = [&](auto&& f) {
+        for (uint32_t i = lane; i < ktot; i += kWave) f(__uint_as_float(lds[i]));
+      };
+      // Value bins over the kept values' own range (all below fhi, so NaN is
+      // never kept; -inf may be).
+      float khi = -__builtin_huge_valf(), klo = __builtin_huge_valf();
       visit_kept([&](float v) {
-        const bool in = value_bin(v, klo, ks, kFinBins - 1) == static_cast<int>(bsel);
-        const uint64_t m = ballot(in);
-        if (in) gl[ng + lanes_below(m)] = __float_as_uint(v);
-        ng += popc64(m);
+        khi = fmaxf(khi, v);
+        klo = fminf(klo, v);
       });
+      khi = wave_extreme_f32<true>(khi);
+      klo = wave_extreme_f32<false>(klo);
+      const float krange = khi - klo;
+      const float ks = static_cast<float>(kFinBins) / krange;
+      // Bins need a finite range (klo > -inf); else all equal or -inf kept.
+      const bool binned = krange > 0.0f && krange <= __FLT_MAX__ && ks <= __FLT_MAX__;
+      uint32_t* fh = lds + kCandCap;
+      reinterpret_cast<uint4*>(fh)[lane] = make_uint4(0u, 0u, 0u, 0u);
       wave_lds_sync();
-      const float mv = lane < static_cast<int>(bcnt) ? __uint_as_float(gl[lane]) : 0.0f;
-      uint32_t gt = 0, ge = 0;
-      for (uint32_t j = 0; j < bcnt; ++j) {
-        const float o = __uint_as_float(gl[j]);
-        gt += (o > mv) ? 1u : 0u;
-        ge += (o >= mv) ? 1u : 0u;
+      if (binned) visit_kept([&](float v) { atomicAdd(&fh[value_bin(v, klo, ks, kFinBins - 1)], 1u); });
+      else if (lane == 0) fh[0] = ktot;  // one bin: the radix passes below
+      wave_lds_sync();
+      // Suffix scan over the bins (4 per lane) for the bin holding rank krem.
+      const uint4 h4 = reinterpret_cast<const uint4*>(fh)[lane];
+      const uint32_t h[4] = {h4.x, h4.y, h4.z, h4.w};
+      const uint32_t local = h[0] + h[1] + h[2] + h[3];
+      const uint32_t incl = wave_inclusive_sum(local);
+      const uint32_t abv = wave_read_lane(incl, kWave - 1) - incl;
+      const bool here = abv < krem && abv + local >= krem;
+      uint32_t bsel = 0, brank = 0, bcnt = 0;
+      if (here) {
+        uint32_t cum = abv;
+  #pragma unroll
+        for (int i = 3; i >= 0; --i) {
+          if (bcnt == 0u && cum + h[i] >= krem) {
+            bsel = 4u * lane + i;
+            brank = krem - cum;
+            bcnt = h[i];
+          }
+          cum += h[i];
+        }
       }
-      const bool hit = lane < static_cast<int>(bcnt) && gt < brank && ge >= brank;
-      res = __int_as_float(wave_read_lane(
-          __float_as_int(mv), __ffsll(static_cast<unsigned long long>(ballot(hit))) - 1));
-    } else {
-      // Heavy ties or no finite range: exact radix passes over the kept keys.
-      const uint32_t tk = wave_select_keys(
-          [&](auto&& f) { visit_kept([&](float v) { f(float_to_key(v)); }); }, 0u, 32, krem, fh);
-      res = key_to_float(tk);
+      const int srcl = __ffsll(static_cast<unsigned long long>(ballot(here))) - 1;
+      bsel = wave_read_lane(bsel, srcl);
+      brank = wave_read_lane(brank, srcl);
+      bcnt = wave_read_lane(bcnt, srcl);
+      float res;
+      if (binned && bcnt <= static_cast<uint32_t>(kFinGather)) {
+        // Gather the chosen bin's values, then rank them against each other:
+        // the wanted one has fewer than brank greater and at least brank
+        // greater-or-equal.
+        uint32_t* gl = fh + kFinBins;
+        uint32_t ng = 0;
+        visit_kept([&](float v) {
+          const bool in = value_bin(v, klo, ks, kFinBins - 1) == static_cast<int>(bsel);
+          const uint64_t m = ballot(in);
+          if (in) gl[ng + lanes_below(m)] = __float_as_uint(v);
+          ng += popc64(m);
+        });
+        wave_lds_sync();
+        const float mv = lane < static_cast<int>(bcnt) ? __uint_as_float(gl[lane]) : 0.0f;
+        uint32_t gt = 0, ge = 0;
+        for (uint32_t j = 0; j < bcnt; ++j) {
+          const float o = __uint_as_float(gl[j]);
+          gt += (o > mv) ? 1u : 0u;
+          ge += (o >= mv) ? 1u : 0u;
+        }
+        const bool hit = lane < static_cast<int>(bcnt) && gt < brank && ge >= brank;
+        res = __int_as_float(wave_read_lane(
+            __float_as_int(mv), __ffsll(static_cast<unsigned long long>(ballot(hit))) - 1));
+      } else {
+        // Heavy ties or no finite range: exact radix passes over the kept keys.
+        const uint32_t tk = wave_select_keys(
+            [&](auto&& f) { visit_kept([&](float v) { f(float_to_key(v)); }); }, 0u, 32, krem, fh);
+        res = key_to_float(tk);
+      }
+      if (lane == 0) {
+        a.thr[row] = res + 0.0f;  // -0 reported as +0, as the key order does
+        rsh[0] = res + 0.0f;
+      }
+    }  // wave 0
+    if constexpr (IDX) {
+      block_sync_lds();
+      const float thr = rsh[0];
+      // This thread's kept values (its kc entries of the kept list, in its
+      // streaming order) above / equal to thr, into its own bytes.
+      uint64_t rem = kpt;
+      for (uint32_t s = 0; s < kc; ++s) {
+        const int bp = static_cast<int>(__builtin_ctzll(rem));
+        rem &= rem - 1u;
+        const int sl = bp >> 2;
+        const int j = sl < 4 ? sample_chunk(sl) : chunk_of(sl - 4);
+        const float v = __uint_as_float(lds[kbase + s]);
+        const uint32_t f = ((v > thr) ? 1u : 0u) | ((v == thr) ? 16u : 0u);
+        fb[j * NT + tid] = static_cast<uint8_t>(fb[j * NT + tid] | (f << (bp & 3)));
+      }
+      block_sync_lds();
+      // Thread t takes positions [64t, 64t+64): one scan of its (above,
+      // equal) counts places them, and it walks its set bits only.  The k
+      // indices are staged in LDS and written out coalesced.
+      const uint4 fv = reinterpret_cast<const uint4*>(fb)[tid];
+      auto nib = [](uint4 v, int sh) {  // nibble `sh` of 16 bytes -> 64 bits
+        auto w16 = [sh](uint32_t w) {
+          w >>= sh;
+          return (w & 0xfu) | ((w >> 4) & 0xf0u) | ((w >> 8) & 0xf00u) | ((w >> 12) & 0xf000u);
+        };
+        return static_cast<uint64_t>(w16(v.x)) | (static_cast<uint64_t>(w16(v.y)) << 16) |
+               (static_cast<uint64_t>(w16(v.z)) << 32) | (static_cast<uint64_t>(w16(v.w)) << 48);
+      };
+      const uint64_t G = nib(fv, 0), Eq = nib(fv, 4);
+      uint32_t tot;
+      const uint32_t ex = block_exclusive_sum<NT>(
+          static_cast<uint32_t>(__builtin_popcountll(G)) |
+              (static_cast<uint32_t>(__builtin_popcountll(Eq)) << 16),
+          wsum, tot);  // its barriers also order the bitmap reads before the staging
+      const uint32_t kq = ku - (tot & 0xffffu);  // equal values taken, lowest positions first
+      int32_t* out = a.idx + row * static_cast<int64_t>(k);
+      const bool staged = k <= kIdxStage;
+      int32_t* so = reinterpret_cast<int32_t*>(lds);
+      uint32_t gb = ex & 0xffffu, eb = ex >> 16;
+      if ((tot >> 16) <= kq) {
+        // Every equal value is taken (the usual case): an entry's slot is its
+        // rank among the selected ones.
+        uint32_t slot = gb + eb;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          for (uint32_t m = static_cast<uint32_t>((G | Eq) >> (32 * h)); m != 0u; m &= m - 1u) {
+            const int32_t pos = 64 * tid + 32 * h + static_cast<int32_t>(__builtin_ctz(m));
+            if (staged) so[slot] = pos;
+            else out[slot] = pos;
+            ++slot;
+          }
+        }
+      } else {
+        for (uint64_t m = G | Eq; m != 0u; m &= m - 1u) {
+          const int bp = static_cast<int>(__builtin_ctzll(m));
+          const int32_t pos = 64 * tid + bp;
+          int32_t slot = -1;
+          if ((G >> bp) & 1u) {
+            slot = static_cast<int32_t>(gb + (eb < kq ? eb : kq));
+            ++gb;
+          } else {
+            if (eb < kq) slot = static_cast<int32_t>(gb + eb);
+            ++eb;
+          }
+          if (slot >= 0) {
+            if (staged) so[slot] = pos;
+            else out[slot] = pos;
+          }
+        }
+      }
+      if (staged) {
+        block_sync_lds();
+        for (int i = tid; i < k; i += NT) out[i] = so[i];
+      }
     }
-    if (lane == 0) a.thr[row] = res + 0.0f;  // -0 reported as +0, as the key order does
     return;
   }
   uint32_t krem;
   const uint32_t tk = stream_select<NT, true>(src, nvalid, k, lds, wsum, info, krem);
   if (tid == 0) a.thr[row] = key_to_float(tk);
+  if constexpr (IDX) {
+    const int64_t nchunks = (nvalid + 4 * NT - 1) / (4 * NT);
+    emit_indices<NT>(a.idx + row * static_cast<int64_t>(k), nchunks, tk, krem, wsum,
+                     [&](int64_t j, uint32_t(&kk)[4]) {
+                       load_keys4<true>(src, (j * NT + tid) * 4, nvalid, kk);
+                     });
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1115,6 +1245,8 @@ hipError_t launch_reg(const SelectArgs& a, bool vec, hipStream_t stream) {
 // The bracket kernel pays off when the keys it keeps fit LDS with room to
 // spare: expected kept keys at the longest row, (2*delta + 1) sample ranks
 // scaled by n/m, at most half of kCandCap.
+constexpr int64_t kBracketIdxMaxN = 16 * 4 * 256;
+
 bool bracket_fits(int64_t cap, int k) {
   if (cap <= 4096 || cap > (int64_t{1} << 20)) return false;
   const double frac = 4096.0 / static_cast<double>(cap);
@@ -1125,7 +1257,10 @@ bool bracket_fits(int64_t cap, int k) {
 
 hipError_t launch_bracket(const SelectArgs& a, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(a.rows));
-  hipLaunchKernelGGL((topk_bracket_kernel<256>), grid, dim3(256), 0, stream, a);
+  if (a.idx != nullptr)
+    hipLaunchKernelGGL((topk_bracket_kernel<256, true>), grid, dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((topk_bracket_kernel<256, false>), grid, dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -1152,11 +1287,14 @@ hipError_t launch_topk(const float* scores, int64_t rows, int64_t n, int64_t ld,
   // Rows above 8K entries use a 12-bit first digit: hot digits of real
   // score rows spread over twice the bins (fewer same-address LDS atomics)
   // and the chosen digit leaves half the candidates.
-  // Threshold-only rows above 4K entries: one pass over HBM (bracket kernel);
-  // up to 2K entries: one wave per row, the row in registers (config 2
+  // Rows above 4K entries: one pass over HBM (bracket kernel);
+  // threshold-only rows up to 2K entries: one wave per row, the row in registers (config 2
   // standalone: 284 -> 224 us; at 4K entries, 64 registers of row per lane
   // leave 4 waves per SIMD and the block kernel is faster: 43 vs 45 us).
-  if (idx == nullptr && vec && bracket_fits(cap, k)) return launch_bracket(a, stream);
+  // With indices: rows of at most 16 chunks (the per-thread position masks
+  // are 64 bits).
+  if (vec && bracket_fits(cap, k) && (idx == nullptr || cap <= kBracketIdxMaxN))
+    return launch_bracket(a, stream);
   if (idx == nullptr && vec && cap <= 2048) {
     if (cap <= 512) return launch_wave<8>(a, stream);
     if (cap <= 1024) return launch_wave<16>(a, stream);

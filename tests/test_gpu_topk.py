@@ -118,6 +118,37 @@ def test_bracket_path_misses_fall_back(dev):
                                    rtol=0, atol=0, equal_nan=True, msg=f"k={k}")
 
 
+@pytest.mark.parametrize("k", [1, 100, 2048, 3000, 16383])
+def test_bracket_indices_single_pass(dev, k):
+    """Thresholds with exactly-k indices of rows up to 16384 entries come from
+    the bracket kernel's single read: the same rows as above (sample misses,
+    one value, three values, ascending, +inf chunk, NaN, -inf halves, wide
+    range, outlier) plus ragged lengths, every index set against the oracle
+    (lowest positions win ties, ascending order)."""
+    n = 16384
+    x = cpu_randn((12, n), 77)
+    x[1, 1024:2048] += 100.0
+    x[2, 1024:4096] -= 100.0
+    x[3] = 1.0
+    x[4] = torch.randint(0, 3, (n,), generator=torch.Generator().manual_seed(4)).float()
+    x[5] = torch.sort(x[5]).values
+    x[6, 4096:5120] = float("inf")
+    x[7, ::97] = float("nan")
+    x[8, : n // 2] = float("-inf")
+    x[9, 100:] = float("-inf")
+    x[10] = x[10] * 1e30
+    x[11, 777] = 3e38
+    say(f"topk bracket+indices k={k}")
+    thr, idx = topk_indices(x.to(dev), k)
+    torch.testing.assert_close(thr.cpu(), O.topk_threshold(x, k), rtol=0, atol=0, equal_nan=True)
+    got = idx.cpu().numpy()
+    want = O.select_indices(x.numpy(), k)
+    bad = np.flatnonzero((got != want).any(-1))
+    assert bad.size == 0, f"rows {bad} with a different index set"
+    for m in (4097, 5000, 9999):
+        check_rows(cpu_randn((3, m), m), min(k, m), dev, what="bracket+indices ragged")
+
+
 def test_reference_extension_test_cases(dev):
     """test_topk_avx512.py:20-35 on the GPU drop-in: torch.equal vs torch.topk."""
     torch.manual_seed(0)
