@@ -207,7 +207,7 @@ def bench_split_long(dev, cfg, dtype, name, reps, fp8_indexer=False):
 
     from dsa_attention import sparse_attention_hip
     from lightning_indexer import indexer_scores_hip
-    from topk_threshold import topk_threshold
+    from topk_threshold import topk_threshold_into
 
     B, T, k = cfg["B"], cfg["T"], cfg["k"]
     ins = gpu_inputs(cfg, dtype, dev, seed=3)
@@ -216,7 +216,7 @@ def bench_split_long(dev, cfg, dtype, name, reps, fp8_indexer=False):
     thr = torch.empty(B, T, 1, device=dev)
     out = torch.empty(B, T, cfg["HQ"], cfg["DV"], device=dev)
     ix = lambda: indexer_scores_hip(*ins[:3], write_upper=False, out=scores)  # noqa: E731
-    sel = lambda: thr.copy_(topk_threshold(scores, min(k, T), causal=True))  # noqa: E731
+    sel = lambda: topk_threshold_into(scores, min(k, T), thr, causal=True)  # noqa: E731
     att = lambda: sparse_attention_hip(scores, thr, *ins[3:], out=out)  # noqa: E731
 
     def fwd():
