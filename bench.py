@@ -636,7 +636,7 @@ def pmc_workload(args, dev):
 
     import dsa_attention as D
     from lightning_indexer import indexer_scores_hip
-    from topk_threshold import topk_threshold
+    from topk_threshold import topk_indices, topk_threshold
 
     x = torch.ones(64 * 1024 * 1024, device=dev)
     y = torch.empty_like(x)
@@ -654,10 +654,12 @@ def pmc_workload(args, dev):
     del q, kk, w
     for _ in range(3):
         thr = topk_threshold(scores, C4["k"], causal=True)
+    for _ in range(2):                                      # thresholds + exactly-k indices
+        topk_indices(scores, C4["k"], causal=True)
     Q, K, V = gpu_inputs(C4, torch.bfloat16, dev, seed=5)[3:]
     out = torch.empty(1, C4["T"], C4["HQ"], C4["DV"], device=dev)
-    for _ in range(2):
-        D.sparse_attention_hip(scores, thr, Q, K, V, out=out)   # the tile kernel at this T
+    for _ in range(2):   # selection bitmask + the tile kernel reading it, at this T
+        D.sparse_attention_hip(scores, thr, Q, K, V, out=out)
     torch.cuda.synchronize()
     del scores, thr, Q, K, V, out
     # config 3: indexer (fp32), select, and 2 launches of the staged attention
