@@ -282,6 +282,8 @@ int dsa_sparse_attn_threshold_staged(const float* scores, int64_t ld, const floa
   if (!dsa::staged_attn_supported(dtype, HQ, DQ, DV))
     return fail(DSA_EUNSUPPORTED, "sparse_attn_staged: needs DQ = DV and HQ*DQ = 256 or 512 (fp32) / 512 (16-bit) (HQ=%d DQ=%d DV=%d dtype %d)", HQ, DQ, DV, dtype);
   if (ld < T) return fail(DSA_EINVAL, "sparse_attn_staged: ld=%lld < T=%lld", (long long)ld, (long long)T);
+  if (!dsa::staged_attn_fits(T, ld))
+    return fail(DSA_EUNSUPPORTED, "sparse_attn_staged: T*ld*4 = %lld bytes of scores per batch element, the limit is 2^31 (use dsa_sparse_attn_threshold)", (long long)(T * ld * 4));
   if (!std::isfinite(scale)) return fail(DSA_EINVAL, "sparse_attn_staged: scale must be finite");
   if (B * T == 0) return DSA_OK;
   if (!scores || !thr) return fail(DSA_EINVAL, "sparse_attn_staged: null pointer");

@@ -289,6 +289,19 @@ __device__ __forceinline__ void load_cvt(const typename Tag::raw* __restrict__ p
   }
 }
 
+// Buffer resource over rows s1 .. T-1 of a [T, rowbytes] array (`base` is
+// row 0).  Its size ends at row T, so buffer reads at or past row T are
+// range-checked by the hardware and return zeros without touching memory;
+// with s1 >= T every read does.  Word 3 is the raw-buffer configuration of
+// CDNA (untyped dword access).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const char* base, int64_t s1, int64_t T,
+                                                           uint32_t rowbytes) {
+  const uint64_t rem = s1 >= T ? 0ull : static_cast<uint64_t>(T - s1) * rowbytes;
+  const int nrec = rem > 0xffffffffull ? -1 : static_cast<int>(static_cast<uint32_t>(rem));
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base + s1 * rowbytes), 0, nrec,
+                                           0x00020000);
+}
+
 // Block order for causal work whose cost grows with the query tile.
 // Workgroups are dispatched in index order, round-robin over the 8 XCDs
 // (block i starts on XCD i % 8).  Index order here is: tiles longest first,

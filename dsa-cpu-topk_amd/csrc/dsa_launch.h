@@ -70,8 +70,22 @@ hipError_t launch_sparse_attn_mask_noalloc(const float* scores, int64_t ld, cons
 // (staged_attn.hip): rows of 64*E elements, DQ = DV, E in {4, 8} for fp32
 // and 8 for 16-bit.  The threshold entry point switches to it at
 // T >= kStagedMinT when it applies and the tile kernel does not.
-constexpr int64_t kStagedMinT = 3072;  // fp32 HQ=8,D=64: gathers win at T=2047 (0.31 vs 0.38 ms), staged at 4096 (0.54 vs 0.69)
+constexpr int64_t kStagedMinT = 3072;
 bool staged_attn_supported(int dtype, int HQ, int DQ, int DV);
+// Whether the threshold entry point takes the staged kernel: fp32 rows of
+// 512 elements (E = 8) only, T >= kStagedMinT, and at least half a block per
+// compute unit (a block streams the keys of two 32-query tiles and fills a
+// CU's LDS; with fewer blocks, or for fp32 rows of 256 elements or 16-bit
+// rows, the per-query gathers were faster on MI355X: e.g. 0.15 vs 0.38 ms at
+// B=2, T=4096, HQ=4, D=64, k=256 fp32; 0.37 vs 0.41 at B=2, T=4096, HQ=8,
+// D=64, k=256; 0.70 vs 0.44 for the staged kernel at B=4).
+bool staged_attn_auto(int dtype, int64_t B, int64_t T, int HQ, int DQ, int DV);
+// Compute units of the current device (cached per thread), 0 if unknown.
+int device_cus();
+// Its score copies address one batch element's [T, ld] rows with 32-bit
+// buffer offsets.
+constexpr int64_t kStagedMaxScoreBytes = int64_t{1} << 31;
+inline bool staged_attn_fits(int64_t T, int64_t ld) { return T * ld * 4 < kStagedMaxScoreBytes; }
 hipError_t launch_staged_attn(const float* scores, int64_t ld, const float* thr, const void* Q,
                               const void* K, const void* V, int dtype, int64_t B, int64_t T,
                               int HQ, int DQ, float scale, float* out, hipStream_t stream);

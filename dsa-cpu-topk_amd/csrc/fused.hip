@@ -235,26 +235,6 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
   }
 }
 
-// Compute units of the current device (cached per thread), 0 if unknown.
-int device_cus() {
-  thread_local int c_dev = -1, c_cus = 0;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) {
-    (void)hipGetLastError();
-    return 0;
-  }
-  if (dev != c_dev) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
-      (void)hipGetLastError();
-      return 0;
-    }
-    c_dev = dev;
-    c_cus = cus;
-  }
-  return c_cus;
-}
-
 template <typename Tag, int DI, int KB, int EK, int EV, int QB>
 hipError_t launch(const FusedArgs& a, hipStream_t stream) {
   const size_t lds = fused_lds_bytes(a.T, QB);
@@ -321,6 +301,26 @@ hipError_t launch_qb(const FusedArgs& a, hipStream_t stream) {
   break;
 
 }  // namespace
+
+// Compute units of the current device (cached per thread), 0 if unknown.
+int device_cus() {
+  thread_local int c_dev = -1, c_cus = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  if (dev != c_dev) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      return 0;
+    }
+    c_dev = dev;
+    c_cus = cus;
+  }
+  return c_cus;
+}
 
 hipError_t launch_fused(const void* qi, const void* ki, const void* wi, const void* Q,
                         const void* K, const void* V, int dtype, int64_t B, int64_t T, int HI,

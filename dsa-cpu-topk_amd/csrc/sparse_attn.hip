@@ -156,7 +156,7 @@ hipError_t launch_sparse_attn(const float* scores, int64_t ld, const float* thr,
     return launch_tile_attn(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, scale, out, stream);
   // Long rows whose K/V rows a wave holds in one slice: each block streams
   // its causal keys once through LDS instead of gathering per query.
-  if (T >= kStagedMinT && staged_attn_supported(dtype, HQ, DQ, DV))
+  if (staged_attn_auto(dtype, B, T, HQ, DQ, DV) && staged_attn_fits(T, ld))
     return launch_staged_attn(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, scale, out, stream);
   return launch_sparse_attn_gather(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, DV, scale,
                                    out, stream);

@@ -9,10 +9,12 @@
 // the per-query gather pulls each query's K/V rows from L2/MALL on its own
 // (16.6 GB per forward at config 3) although the selected sets of nearby
 // queries are spread over the same key range.  Here a block streams its
-// causal key range once, in tiles of 16 KiB of K rows (8 or 16 keys) copied
-// HBM/L2 -> LDS by the DMA path (global_load_lds, a ring of 4 slots, 3 tiles
-// ahead), and every wave computes its queries' selected pairs of the tile
-// from LDS.
+// causal key range once, in tiles of 16 keys copied HBM/L2 -> LDS by the DMA
+// path (buffer_load ... lds through range-checked buffer resources whose
+// base moves with the tile, so a copy costs no per-lane address arithmetic;
+// a ring of 4 slots, 3 tiles ahead, for rows of 1 KiB, and of 2 slots, 1
+// tile ahead, for rows of 2 KiB), and every wave computes its queries'
+// selected pairs of the tile from LDS.
 //
 // Block = 16 waves = two 32-query tiles of one batch element, tile p and
 // tile ntile-1-p, so every block has about the same causal work (T keys x 32
@@ -23,17 +25,20 @@
 // reads the key's K and V slices from LDS once and updates each selecting
 // query.
 //
-// Measured at config 3 (B=4, T=4096, k=256, HQ=8, D=64, fp32): 0.54 ms
-// against 0.69-0.75 ms for per-query gathers; at T=2047 the gathers are
-// faster (0.31 vs 0.38 ms), so the threshold entry point switches at 3072.
+// Measured at config 3 (B=4, T=4096, k=256, HQ=8, D=64, fp32): 0.438 ms
+// against 0.69-0.75 ms for per-query gathers (8-key tiles in a ring of 4:
+// 0.497 ms; with per-lane address arithmetic for the copies: 0.544 ms).
 // What limits it: the barrier per key tile waits for the busiest wave (the
-// selected pairs per wave and tile vary about 1.7x around their mean).
+// selected pairs per wave and tile vary about 1.7x around their mean for
+// 8-key tiles); 16-key tiles average the variation over twice the pairs.
+// The threshold entry point takes this kernel only where it measured faster
+// than the gathers (staged_attn_auto).
 //
 // Lane layout as in attn_tile.h: a K (or V) row is 64*E elements, lane l
 // owns [l*E, (l+1)*E); a head spans DQ/E lanes and its logit is a butterfly
 // over them.  Softmax is online in the log2 domain with fp32 state; the
-// running max moves only when a logit exceeds it by more than 2^8, so the
-// accumulator is rescaled on a few keys per query.  Rows that select
+// running max moves only when a logit exceeds it by more than 8 (a factor
+// 2^8), so the accumulator is rescaled on a few keys per query.  Rows that select
 // nothing output NaN (0/0), as the reference.
 #include <type_traits>
 
@@ -44,8 +49,6 @@ namespace dsa {
 namespace {
 
 constexpr int kSTQ = 32;     // queries per tile; a block holds two tiles
-constexpr int kSlots = 4;    // LDS ring of key tiles: DMA runs 3 tiles ahead
-constexpr int kSlotK = 16384;  // bytes of K (and of V) per key tile
 
 #define DSA_LDS __attribute__((address_space(3)))
 
@@ -66,9 +69,15 @@ struct StagedArgs {
 
 template <typename Tag, int E>
 constexpr int row_bytes() { return kWave * E * Tag::kBytes; }
-// Keys per LDS tile: 16 KiB of K rows (8 keys of 512 fp32, 16 otherwise).
+// Bytes of K (and of V) per key tile: 16 keys per tile.  A tile of 16 keys
+// holds 16 KiB of K for rows of 1 KiB and 32 KiB for rows of 2 KiB (fp32,
+// 512 elements); the LDS ring then has 4 or 2 slots.
 template <typename Tag, int E>
-constexpr int tile_keys() { return kSlotK / row_bytes<Tag, E>(); }
+constexpr int slot_bytes() { return 16 * row_bytes<Tag, E>(); }
+template <typename Tag, int E>
+constexpr int tile_keys() { return slot_bytes<Tag, E>() / row_bytes<Tag, E>(); }
+template <typename Tag, int E>
+constexpr int ring_slots() { return slot_bytes<Tag, E>() <= 16384 ? 4 : 2; }
 
 // LDS row layout.  A lane reads its slice of a row as E*bytes/16 chunks of
 // 16 bytes.  With one chunk per lane the row is stored as is (lane l reads
@@ -88,28 +97,27 @@ __device__ __forceinline__ int logical_chunk(int pc, int cpr) {
   else return pc;
 }
 
-// Copies rows s0 .. s0+KT-1 of one batch element's [T, 64E] K or V into
-// dst (rows past T repeat row T-1; they are never selected) with the NT
-// threads of the block, in the LDS row layout above.  Physical chunk c of
-// the tile (16 bytes) lands at dst + 16c: each wave instruction fills 1 KiB.
-template <typename Tag, int E, int NT, int KT>
-__device__ __forceinline__ void dma_rows(const char* __restrict__ src, int s0, int T,
-                                         DSA_LDS uint8_t* dst, int tid) {
+// Byte offset, within a key tile of rows of RB bytes, of physical chunk c
+// (16 bytes), which lands at LDS offset 16c in the row layout above: thread
+// tid copies chunks tid, tid + NT, ..., so each wave instruction fills 1 KiB.
+template <typename Tag, int E>
+__device__ __forceinline__ uint32_t tile_chunk_offset(int c) {
   constexpr int RB = row_bytes<Tag, E>();
-  constexpr int NCH = KT * RB / 16;
   constexpr int CPR = RB / 16;  // chunks per row
-#pragma unroll
-  for (int c0 = 0; c0 < NCH; c0 += NT) {
-    if (c0 + (tid & ~(kWave - 1)) < NCH) {  // whole waves only
-      const int c = c0 + tid;
-      const int r = c / CPR;
-      const uint32_t s = static_cast<uint32_t>(min(s0 + r, T - 1));
-      const int lc = logical_chunk<chunks_per_lane<Tag, E>()>(c % CPR, CPR);
-      const uint32_t off = s * static_cast<uint32_t>(RB) + 16u * static_cast<uint32_t>(lc);
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(src + off),
-                                       dst + (c0 + (tid & ~(kWave - 1))) * 16, 16, 0, 0);
-    }
-  }
+  const int lc = logical_chunk<chunks_per_lane<Tag, E>()>(c % CPR, CPR);
+  return static_cast<uint32_t>((c / CPR) * RB + 16 * lc);
+}
+
+// Buffer resource over elements s0 .. n-1 of an array of `bytes`-sized
+// elements (`base` is element 0; no element when s0 >= n): reads past
+// element n-1 are range-checked by the hardware and return zeros.  The
+// callers keep n * bytes below 2^31, so the size is 32-bit scalar
+// arithmetic.  Word 3 is the raw-buffer configuration of CDNA.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t span_rsrc(const char* base, int s0, int n,
+                                                           int bytes) {
+  const int rem = s0 >= n ? 0 : (n - s0) * bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base) + static_cast<int64_t>(s0) * bytes,
+                                           0, rem, 0x00020000);
 }
 
 // This lane's E elements of an LDS row (layout above), as fp32.
@@ -144,16 +152,16 @@ __device__ __forceinline__ void lds_slice(const DSA_LDS uint8_t* row, int lane, 
 // butterfly is straight-line code.  QPW: queries per wave (QPW/2 from each
 // tile); the block has 64/QPW waves.
 //
-// Pipeline: kSlots LDS slots, each holding one key tile's K rows, V rows and
-// the block's scores for it, all copied by DMA.  Iteration kt waits for
-// tile kt's copies, passes one barrier (every wave is then done with tile
-// kt-1, whose slot is free), issues the copies of tile kt+3 into that slot
-// and computes tile kt.  Every iteration issues the same copies (tiles past
-// the end copy clamped rows into a slot nobody reads), so the wait is one
-// fixed vmcnt: all but the 2 tiles' copies issued after tile kt's.  The
-// slots are separate LDS objects and the loop is unrolled over them, so the
-// compiler sees that a copy into one slot does not alias reads of another
-// and leaves the copies in flight.
+// Pipeline: NS LDS slots (ring_slots), each holding one key tile's K rows,
+// V rows and the block's scores for it, all copied by DMA.  Iteration kt
+// waits for tile kt's copies, passes one barrier (every wave is then done
+// with tile kt-1, whose slot is free), issues the copies of tile kt+NS-1
+// into that slot and computes tile kt.  Every iteration issues the same
+// copies (tiles past the end read as zeros into a slot nobody reads), so the
+// wait is one fixed vmcnt: all but the copies of the NS-2 tiles issued after
+// tile kt's.  The slots are separate LDS objects and the loop is unrolled
+// over them, so the compiler sees that a copy into one slot does not alias
+// reads of another and leaves the copies in flight.
 template <typename Tag, int E, int LPH, int QPW>
 __global__ __launch_bounds__(64 / QPW * kWave) void staged_attn_kernel(StagedArgs a) {
   static_assert(QPW == 4 || QPW == 8, "4 or 8 queries per wave");
@@ -163,30 +171,34 @@ __global__ __launch_bounds__(64 / QPW * kWave) void staged_attn_kernel(StagedArg
   constexpr int KT = tile_keys<Tag, E>();
   static_assert(KT == 8 || KT == 16, "8 or 16 keys per tile");
   static_assert(QPW * KT <= kWave, "one score per lane per tile");
-  constexpr int DKV = 2 * ((kSlotK / 16 + NT - 1) / NT);  // K and V copy instructions per tile
-  constexpr int WAITN = 2 * (DKV + 1);                    // + 1 score copy per tile
+  constexpr int SK = slot_bytes<Tag, E>();
+  constexpr int NS = ring_slots<Tag, E>();
+  constexpr int CH = SK / 16 / NT;  // 16-byte chunks of K (and of V) per thread and tile
+  static_assert(CH * 16 * NT == SK && (CH == 1 || CH == 2), "whole chunks per thread");
+  constexpr int WAITN = (NS - 2) * (2 * CH + 1);  // copies of the tiles issued after tile kt
   static_assert(WAITN <= 63, "vmcnt field");
   using raw = typename Tag::raw;
   constexpr int RB = row_bytes<Tag, E>();
   constexpr int RE = kWave * E;  // elements per K/V row
   constexpr int SCB = NW * kWave * 4;  // score bytes per tile (one float per lane)
-  // One LDS object per slot (K rows, V rows, scores): four objects keep the
-  // compiler's tracking of copies in flight exact.
+  // One LDS object per slot (K rows, V rows, scores): separate objects keep
+  // the compiler's tracking of copies in flight exact.  With a ring of 2,
+  // slots 2 and 3 are never referenced and take no LDS.
   struct Slot {
-    uint8_t k[kSlotK];
-    uint8_t v[kSlotK];
+    uint8_t k[SK];
+    uint8_t v[SK];
     uint8_t c[SCB];
   };
   __shared__ __align__(16) Slot sl0, sl1, sl2, sl3;
-  DSA_LDS uint8_t* ks[kSlots] = {(DSA_LDS uint8_t*)sl0.k, (DSA_LDS uint8_t*)sl1.k,
-                                 (DSA_LDS uint8_t*)sl2.k, (DSA_LDS uint8_t*)sl3.k};
-  DSA_LDS uint8_t* vs[kSlots] = {(DSA_LDS uint8_t*)sl0.v, (DSA_LDS uint8_t*)sl1.v,
-                                 (DSA_LDS uint8_t*)sl2.v, (DSA_LDS uint8_t*)sl3.v};
-  DSA_LDS uint8_t* cs[kSlots] = {(DSA_LDS uint8_t*)sl0.c, (DSA_LDS uint8_t*)sl1.c,
-                                 (DSA_LDS uint8_t*)sl2.c, (DSA_LDS uint8_t*)sl3.c};
+  DSA_LDS uint8_t* ks[4] = {(DSA_LDS uint8_t*)sl0.k, (DSA_LDS uint8_t*)sl1.k,
+                            (DSA_LDS uint8_t*)sl2.k, (DSA_LDS uint8_t*)sl3.k};
+  DSA_LDS uint8_t* vs[4] = {(DSA_LDS uint8_t*)sl0.v, (DSA_LDS uint8_t*)sl1.v,
+                            (DSA_LDS uint8_t*)sl2.v, (DSA_LDS uint8_t*)sl3.v};
+  DSA_LDS uint8_t* cs[4] = {(DSA_LDS uint8_t*)sl0.c, (DSA_LDS uint8_t*)sl1.c,
+                            (DSA_LDS uint8_t*)sl2.c, (DSA_LDS uint8_t*)sl3.c};
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases stay scalar
   const int lane = lane_id();
   const int T = a.T;
   const int64_t b = static_cast<int64_t>(blockIdx.x) % a.B;
@@ -209,26 +221,51 @@ __global__ __launch_bounds__(64 / QPW * kWave) void staged_attn_kernel(StagedArg
   const bool v_l = i_l < QPW && t_l < T && (i_l < HALF || tb != ta);
   const int tc_l = min(t_l, T - 1);
   const float thr_l = a.thr[b * T + tc_l];
-  const char* srow = reinterpret_cast<const char*>(a.scores + (b * T + tc_l) * a.ld);
-  const int64_t s_clamp = a.ld - 1;
+  // key s0 + j_l is causal for this lane's query iff s0 <= lim_l (never for
+  // lanes without a query)
+  const int lim_l = v_l ? t_l - j_l : -1;
 
+  // Copies go through buffer resources whose base moves with the tile (a
+  // scalar computation): the per-lane offsets below are loop-invariant.  K
+  // and V rows at or past T read as zeros (the resource ends at row T); they
+  // are never causal.  A lane's score is element (tc_l, s0 + j_l) of this
+  // batch element's [T, ld] rows; entries past the row's causal end read
+  // whatever follows (the next row, or zeros past the last) and are masked
+  // by lim_l.  The host keeps T*ld*4 below 2^31.
+  uint32_t kv_off[CH];
+#pragma unroll
+  for (int r = 0; r < CH; ++r) kv_off[r] = tile_chunk_offset<Tag, E>(tid + r * NT);
+  const uint32_t sc_off = static_cast<uint32_t>(tc_l) * static_cast<uint32_t>(a.ld) * 4u +
+                          4u * static_cast<uint32_t>(j_l);
   const char* Kb = static_cast<const char*>(a.K) + b * T * static_cast<int64_t>(RB);
   const char* Vb = static_cast<const char*>(a.V) + b * T * static_cast<int64_t>(RB);
-  auto copy_tile = [&](auto slot_c, int t) {
+  const char* Sb = reinterpret_cast<const char*>(a.scores + b * T * a.ld);
+  const int sc_elems = T * static_cast<int>(a.ld);  // < 2^29
+  auto copy_tile = [&](auto slot_c, int t) __attribute__((always_inline)) {
     constexpr int S = decltype(slot_c)::value;
-    dma_rows<Tag, E, NT, KT>(Kb, t * KT, T, ks[S], tid);
-    dma_rows<Tag, E, NT, KT>(Vb, t * KT, T, vs[S], tid);
-    const int64_t s = min<int64_t>(static_cast<int64_t>(t) * KT + j_l, s_clamp);
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(srow + 4 * s),
-                                     cs[S] + wave * (kWave * 4), 4, 0, 0);
+    const int s0 = t * KT;
+    const __amdgpu_buffer_rsrc_t rk = span_rsrc(Kb, s0, T, RB);
+    const __amdgpu_buffer_rsrc_t rv = span_rsrc(Vb, s0, T, RB);
+#pragma unroll
+    for (int r = 0; r < CH; ++r) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, ks[S] + r * NT * 16 + wave * 1024, 16,
+                                               static_cast<int>(kv_off[r]), 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, vs[S] + r * NT * 16 + wave * 1024, 16,
+                                               static_cast<int>(kv_off[r]), 0, 0, 0);
+    }
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(span_rsrc(Sb, s0, sc_elems, 4),
+                                             cs[S] + wave * (kWave * 4), 4,
+                                             static_cast<int>(sc_off), 0, 0, 0);
   };
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
   using S2 = std::integral_constant<int, 2>;
   using S3 = std::integral_constant<int, 3>;
   copy_tile(S0{}, 0);
-  copy_tile(S1{}, 1);
-  copy_tile(S2{}, 2);
+  if constexpr (NS == 4) {
+    copy_tile(S1{}, 1);
+    copy_tile(S2{}, 2);
+  }
 
   // Query slices (times scale_log2).
   const raw* Qb = static_cast<const raw*>(a.Q) + b * T * static_cast<int64_t>(RE);
@@ -241,11 +278,14 @@ __global__ __launch_bounds__(64 / QPW * kWave) void staged_attn_kernel(StagedArg
     for (int e = 0; e < E; ++e) q[i][e] *= a.scale_log2;
   }
 
+  // mp = running max + 8: a logit moves it only when it exceeds mp, and the
+  // weights exp2(x - mp) are the usual exp2(x - max) times 2^-8, a factor
+  // that cancels in acc / l.
   float acc[QPW][E];
-  float m[QPW], l[QPW];
+  float mp[QPW], l[QPW];
 #pragma unroll
   for (int i = 0; i < QPW; ++i) {
-    m[i] = -__builtin_huge_valf();
+    mp[i] = -__builtin_huge_valf();
     l[i] = 0.f;
 #pragma unroll
     for (int e = 0; e < E; ++e) acc[i][e] = 0.f;
@@ -280,8 +320,8 @@ __global__ __launch_bounds__(64 / QPW * kWave) void staged_attn_kernel(StagedArg
     const float sc = *reinterpret_cast<const DSA_LDS float*>(cs[S] + wave * (kWave * 4) + lane * 4);
     // bit i*KT + j: query i of the wave selects key s0 + j (NaN scores and
     // thresholds select nothing)
-    const uint64_t sel = ballot(v_l && s0 + j_l <= t_l && sc >= thr_l);
-    copy_tile(std::integral_constant<int, (S + 3) % kSlots>{}, kt + 3);
+    const uint64_t sel = ballot((s0 <= lim_l) & (sc >= thr_l));
+    copy_tile(std::integral_constant<int, (S + NS - 1) % NS>{}, kt + NS - 1);
     uint32_t u;
     if constexpr (KT == 16) u = static_cast<uint32_t>((sel | (sel >> 16) | (sel >> 32) | (sel >> 48)) & 0xffffu);
     else u = static_cast<uint32_t>((sel | (sel >> 8) | (sel >> 16) | (sel >> 24)) & 0xffu);
@@ -295,17 +335,17 @@ __global__ __launch_bounds__(64 / QPW * kWave) void staged_attn_kernel(StagedArg
 #pragma unroll
           for (int e = 0; e < E; ++e) x = fmaf(q[i][e], kv[e], x);
           x = head_sum(x);
-          const bool up = x > m[i] + 8.f;
+          const bool up = x > mp[i];
           if (ballot(up) != 0u) {
-            const float mn = up ? x : m[i];
-            const float alpha = exp2f(m[i] - mn);  // m = -inf: 0 on an empty state
+            const float mn = up ? x + 8.f : mp[i];
+            const float alpha = exp2f(mp[i] - mn);  // mp = -inf: 0 on an empty state
             l[i] *= alpha;
 #pragma unroll
             for (int e = 0; e < E; ++e) acc[i][e] *= alpha;
-            m[i] = mn;
+            mp[i] = mn;
           }
           // bare v_exp_f32: results below 2^-126 flush to 0, which no sum can see
-          const float pr = __builtin_amdgcn_exp2f(x - m[i]);
+          const float pr = __builtin_amdgcn_exp2f(x - mp[i]);
           l[i] += pr;
 #pragma unroll
           for (int e = 0; e < E; ++e) acc[i][e] = fmaf(pr, vv[e], acc[i][e]);
@@ -337,7 +377,8 @@ __global__ __launch_bounds__(64 / QPW * kWave) void staged_attn_kernel(StagedArg
       }
     } else {
       // 8 elements per lane: no registers for a second key's slices
-      for (int j = pop(); j >= 0; j = pop()) {
+      for (; u != 0u; u &= u - 1u) {
+        const int j = __builtin_ctz(u);
         float ka[E], va[E];
         lds_slice<Tag, E>(kl + j * RB, lane, ka);
         lds_slice<Tag, E>(vl + j * RB, lane, va);
@@ -346,14 +387,16 @@ __global__ __launch_bounds__(64 / QPW * kWave) void staged_attn_kernel(StagedArg
     }
   };
   // Four tiles per trip: one per slot.
-  for (int kt = 0; kt < nkt; kt += kSlots) {
+  for (int kt = 0; kt < nkt; kt += NS) {
     tile(S0{}, kt);
     if (kt + 1 >= nkt) break;
     tile(S1{}, kt + 1);
-    if (kt + 2 >= nkt) break;
-    tile(S2{}, kt + 2);
-    if (kt + 3 >= nkt) break;
-    tile(S3{}, kt + 3);
+    if constexpr (NS == 4) {
+      if (kt + 2 >= nkt) break;
+      tile(S2{}, kt + 2);
+      if (kt + 3 >= nkt) break;
+      tile(S3{}, kt + 3);
+    }
   }
   // the copies issued past the end must land before the block exits
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -401,10 +444,18 @@ bool staged_attn_supported(int dtype, int HQ, int DQ, int DV) {
   return false;
 }
 
+bool staged_attn_auto(int dtype, int64_t B, int64_t T, int HQ, int DQ, int DV) {
+  if (dtype != 0 || T < kStagedMinT || !staged_attn_supported(dtype, HQ, DQ, DV)) return false;
+  if (static_cast<int64_t>(HQ) * DQ != 8 * kWave) return false;  // E = 8
+  const int64_t blocks = B * (((T + kSTQ - 1) / kSTQ + 1) / 2);
+  return 2 * blocks >= device_cus();
+}
+
 hipError_t launch_staged_attn(const float* scores, int64_t ld, const float* thr, const void* Q,
                               const void* K, const void* V, int dtype, int64_t B, int64_t T,
                               int HQ, int DQ, float scale, float* out, hipStream_t stream) {
   if (B == 0 || T == 0) return hipSuccess;
+  if (!staged_attn_fits(T, ld)) return hipErrorInvalidValue;
   StagedArgs a{scores, ld, thr, Q, K, V, B, static_cast<int>(T), DQ,
                scale * 1.4426950408889634f, out, static_cast<int>((T + kSTQ - 1) / kSTQ)};
   const int E = static_cast<int>(static_cast<int64_t>(HQ) * DQ / kWave);

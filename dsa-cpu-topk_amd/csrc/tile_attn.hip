@@ -149,17 +149,13 @@ struct TileLds {
 };
 
 // Buffer resource over one head's K or V rows from row s1 on (`head_base`
-// is row 0 of this batch element at this head's columns).  Its size ends at
-// row T, so DMA reads of rows at or past T are range-checked by the
-// hardware and return zeros: no per-row clamp.  Those rows are never causal
-// for any query, so they are masked to -inf and their zero V rows add 0.
+// is row 0 of this batch element at this head's columns): rows_rsrc, whose
+// size ends at row T, so DMA reads of rows at or past T return zeros with no
+// per-row clamp.  Those rows are never causal for any query, so they are
+// masked to -inf and their zero V rows add 0.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const char* head_base, int s1, int T,
                                                           uint32_t rowbytes) {
-  const uint64_t rem = static_cast<uint64_t>(T - s1) * rowbytes;
-  const int nrec = rem > 0xffffffffull ? -1 : static_cast<int>(static_cast<uint32_t>(rem));
-  // word 3: the raw-buffer configuration of CDNA (untyped dword access)
-  return __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<char*>(head_base + static_cast<int64_t>(s1) * rowbytes), 0, nrec, 0x00020000);
+  return rows_rsrc(head_base, s1, T, rowbytes);
 }
 
 // Issue this wave's share of the DMA of one 64-row tile into `dst`: PW

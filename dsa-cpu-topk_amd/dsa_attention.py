@@ -82,7 +82,8 @@ def sparse_attention_hip(scores: torch.Tensor, threshold: torch.Tensor, Q, K, V,
 
     The library picks the kernel: per-query gathers; dense-masked MFMA tiles
     for T >= 4096 with 16-bit Q/K/V and DQ = DV in {64, 128}; K/V staged
-    through LDS for other long rows it covers (T >= 3072).  Where it would
+    through LDS for fp32 rows of HQ*DQ = 512 at T >= 3072 when the batch
+    gives at least half a block (two 32-query tiles) per compute unit.  Where it would
     take the tiles, the selection is first reduced to a bitmask
     (dsa_selection_mask, 1 bit per (query, key) instead of a 4-byte score
     read once per head) and the tile kernel reads that (dsa_sparse_attn_mask):

@@ -146,7 +146,8 @@ int dsa_topk_threshold(const float* scores, int64_t rows, int64_t n, int64_t ld,
  * Kernels (chosen by shape, same sel and O): per-query gathers; rows wider
  *   than one wave holds (fp32 HQ*D > 1024, 16-bit > 2048) in head chunks;
  *   the tile kernel below for 16-bit DQ = DV in {64,128} at T >= 4096 or on
- *   wide rows; the staged kernel below for long rows (T >= 3072) it covers.
+ *   wide rows; the staged kernel below for fp32 rows of HQ*DQ = 512 at
+ *   T >= 3072 when the batch gives at least half a block per compute unit.
  * Constraints: HQ, DQ, DV powers of two; a single head of at most 64*16
  *   (fp32) or 64*32 (16-bit) elements; T*HQ*max(DQ,DV)*bytes < 4 GiB;
  *   ld >= T.
@@ -178,18 +179,21 @@ int dsa_sparse_attn_threshold_tiled(const float* scores, int64_t ld, const float
 /*
  * dsa_sparse_attn_threshold with each block's causal K/V rows staged through
  * LDS: a block streams the keys of two 32-query tiles (a long and a short
- * one) once, in tiles of 8 or 16 keys copied by DMA, and every wave computes its
+ * one) once, in tiles of 16 keys copied by DMA, and every wave computes its
  * queries' selected pairs from LDS -- nearby queries select over the same
  * key range, so the K/V bytes read from L2/MALL drop by the block's query
  * count compared with per-query gathers.  dsa_sparse_attn_threshold switches
- * to it by itself for T >= 3072 when the shape qualifies (and the tile
- * kernel does not); this entry point runs it at any T.  Same sel and O,
+ * to it by itself for fp32 rows of HQ*DQ = 512 at T >= 3072 when
+ * B * ceil(ceil(T/32)/2) blocks give at least half a block per compute unit
+ * (other shapes measured faster with the gathers); this entry point runs it
+ * at any T.  Same sel and O,
  * fp32 arithmetic (the softmax sums in a different order than the gathers).
  * Replaces: _sparse_attn_kernel + sparse_attention_with_threshold_triton,
  *           reference dsa_attention.py:234-324 (same contract as above).
  * Constraints: DQ = DV; HQ*DQ = 256 or 512 (fp32) or 512 (bf16/fp16) with
- *   DQ a multiple of HQ*DQ/64; ld >= T; Q, K, V, out 16-byte aligned.
- *   Other shapes return DSA_EUNSUPPORTED.
+ *   DQ a multiple of HQ*DQ/64; ld >= T; T*ld*4 < 2^31 (one batch element's
+ *   score rows are addressed with 32-bit offsets); Q, K, V, out 16-byte
+ *   aligned.  Other shapes return DSA_EUNSUPPORTED.
  */
 int dsa_sparse_attn_threshold_staged(const float* scores, int64_t ld, const float* thr,
                                      const void* Q, const void* K, const void* V,

@@ -346,3 +346,20 @@ def test_indexer_asserts_match_reference():
 
     with pytest.raises(AssertionError):
         indexer_scores_triton(torch.zeros(1, 8, 2, 16), torch.zeros(1, 8, 16), torch.zeros(1, 8, 2))
+
+
+def test_staged_entry_score_limit():
+    """dsa_sparse_attn_threshold_staged addresses one batch element's score
+    rows with 32-bit offsets: T*ld*4 >= 2^31 is refused before any HIP call
+    (the threshold entry point takes the gathers there); B = 0 launches
+    nothing."""
+    f = L.lib().dsa_sparse_attn_threshold_staged
+    T = 16384
+    ok = [FAKE, T, FAKE, FAKE, FAKE, FAKE, L.DSA_F32, 1, T, 8, 64, 64, 0.125, FAKE, None]
+    a = list(ok)
+    a[1] = 2 * T                                         # 16384 x 32768 x 4 = 2^31 bytes
+    rc, msg = _rc(f, *a)
+    assert rc == L.DSA_EUNSUPPORTED and "2^31" in msg, (rc, msg)
+    a = list(ok)
+    a[7] = 0
+    assert f(*a) == L.DSA_OK

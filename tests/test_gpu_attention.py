@@ -368,11 +368,13 @@ def test_staged_and_gather_agree(dev):
 
 
 def test_staged_auto_at_config3_shape(dev):
-    """T = 4096 fp32, HQ = 8, D = 64 (config 3's attention): the threshold
-    entry point runs the staged kernel; sampled rows against the oracle."""
+    """B = 4, T = 4096 fp32, HQ = 8, D = 64 (config 3's attention): the
+    threshold entry point runs the staged kernel (256 blocks of two 32-query
+    tiles: at least half a block per compute unit); sampled rows against the
+    oracle."""
     from helpers import sample_rows
 
-    B, T, HQ, D, k = 1, 4096, 8, 64, 256
+    B, T, HQ, D, k = 4, 4096, 8, 64, 256
     _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, HQ, D, D, seed0=12)
     scores = torch.randn(B, T, T, generator=torch.Generator().manual_seed(2))
     thr = kth(k)(scores)
