@@ -7,10 +7,18 @@
 // index order.
 //
 // Design (gfx950): one workgroup per row, the row read from HBM exactly once
-// straight into registers as order-preserving radix keys (V keys per thread,
-// float4 loads, chunk-major so each load instruction is one contiguous
-// 16*NT-byte span; chunks past the row's valid length are skipped
-// block-uniformly).  Then MSD radix passes over 11/11/10-bit digits:
+// straight into registers (V values per thread, float4 loads, chunk-major so
+// each load instruction is one contiguous 16*NT-byte span; chunks past the
+// row's valid length are skipped block-uniformly).  Rows of up to 16 values
+// per thread first try value bins: the row's min and max (one block
+// reduction), a 512-bin histogram linear in value between them, the bin
+// holding the k-th largest (usually a few values) appended to an LDS list and
+// ranked by key in one wave.  Bins follow the data's density, so the
+// histogram's LDS atomics rarely collide and the finish has a few values to
+// rank; this takes fewer VALU instructions per value than the digit passes
+// below (config 3's causal rows of 1..4096: 44 -> 38 us).  A bin of more than
+// kCandCap values (heavy ties) and longer register rows take MSD radix passes
+// over order-preserving keys, 11/11/10-bit digits:
 //   pass 1  histogram of key[31:21] in LDS (ds_add), block suffix-scan picks
 //           the digit holding the k-th key;
 //           if that digit holds <= kCandCap keys they are compacted into LDS
@@ -337,11 +345,13 @@ __global__ __launch_bounds__(NT, (V <= 32 && NT <= 512) ? 8 : 4) void topk_reg_k
   constexpr int S2 = S1 - B2;           // shift of digit 2
   constexpr int B3 = S2;                // bits of digit 3 (shift 0)
   constexpr int NBINS = 1 << (P1 > B2 ? P1 : B2);
-  __shared__ uint32_t hist[NBINS];
-  __shared__ uint32_t cand[kCandCap];
+  __shared__ __align__(16) uint32_t hist[NBINS];
+  constexpr int CAP = kCandCap;
+  __shared__ uint32_t cand[CAP];
   __shared__ uint32_t wsum[NT / kWave];
   __shared__ uint32_t info[4];
   __shared__ uint32_t ncand;
+  __shared__ float red[3 * (NT / kWave)];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -361,9 +371,10 @@ __global__ __launch_bounds__(NT, (V <= 32 && NT <= 512) ? 8 : 4) void topk_reg_k
   // last entry) instead of predicated, so no load sits behind a branch -- a
   // per-chunk branch made every load wait for the previous one.  Chunks past
   // nch read that one clamped address and are never visited.
+  // The row as float bit patterns (key order is formed only where needed).
   uint32_t key[V];
+  const int nv = static_cast<int>(nvalid);  // the host checks n < 2^31
   {
-    const int nv = static_cast<int>(nvalid);  // the host checks n < 2^31
     // 32-bit byte offsets from the row base (a register row is < 2^30 bytes),
     // so each load takes one offset register against the scalar base
     const char* row_bytes = reinterpret_cast<const char*>(src);
@@ -389,20 +400,42 @@ __global__ __launch_bounds__(NT, (V <= 32 && NT <= 512) ? 8 : 4) void topk_reg_k
           raw[4 * j + c] = *reinterpret_cast<const float*>(row_bytes + off);
         }
     }
-    // Entries past the row become kKeyNone; only a chunk the row ends inside
-    // needs the per-entry test (block-uniform branch after the conversion,
-    // so no load is sunk into it).
+#pragma unroll
+    for (int j = 0; j < V; ++j) key[j] = __float_as_uint(raw[j]);
+  }
+  // f(x, i) for every valid entry: x its value, i its register (chunks past
+  // nch hold clamped duplicates; only the chunk the row ends inside tests
+  // positions).
+  auto visit_vals = [&](auto&& f) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      if (j < nch) {
+        if ((j + 1) * NT * 4 <= nv) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) f(__uint_as_float(key[4 * j + c]), 4 * j + c);
+        } else {
+          const int p0 = (j * NT + tid) * 4;
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (p0 + c < nv) f(__uint_as_float(key[4 * j + c]), 4 * j + c);
+        }
+      }
+    }
+  };
+  // Registers -> radix keys in place; entries past the row become kKeyNone
+  // (only a chunk the row ends inside needs the per-entry test).
+  auto to_keys = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) key[4 * j + c] = float_to_key(raw[4 * j + c]);
+      for (int c = 0; c < 4; ++c) key[4 * j + c] = float_to_key(__uint_as_float(key[4 * j + c]));
       if ((j + 1) * NT * 4 > nv) {
 #pragma unroll
         for (int c = 0; c < 4; ++c)
           if ((j * NT + tid) * 4 + c >= nv) key[4 * j + c] = kKeyNone;
       }
     }
-  }
+  };
   auto visit_regs = [&](auto&& f) {
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
@@ -413,71 +446,211 @@ __global__ __launch_bounds__(NT, (V <= 32 && NT <= 512) ? 8 : 4) void topk_reg_k
     }
   };
 
-  // The first pass tests for kKeyNone only in the chunk the row ends inside.
-  auto visit_first = [&](auto&& f) {
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      if (j < nch) {
-        if ((j + 1) * NT * 4 <= nvalid) {
-#pragma unroll
-          for (int c = 0; c < 4; ++c) f(key[4 * j + c]);
-        } else {
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            if (key[4 * j + c] != kKeyNone) f(key[4 * j + c]);
-        }
-      }
-    }
-  };
-
+  uint32_t thr_key = 0, krem = 0;
+  bool keys_in_regs = false, done = false;
   if (tid == 0) ncand = 0u;
-  uint32_t prefix = 0, krem = static_cast<uint32_t>(k), cnt = 0, thr_key = 0;
-  bool found = radix_pass<NT, S1, P1, true>(visit_first, hist, wsum, info, prefix, krem, cnt,
-                                            true, thr_key);
-  if (!found) {
-    if (cnt <= static_cast<uint32_t>(kCandCap)) {
-      // Compact the chosen digit's keys into LDS: per-lane count, wave scan,
-      // one LDS atomic per wave for the wave's base.
-      const uint32_t top = prefix;
-      uint32_t mine = 0;
-      visit_regs([&](uint32_t kk) { mine += ((kk >> S1) == top) ? 1u : 0u; });
-      const uint32_t incl = wave_inclusive_sum(mine);
-      const uint32_t wtot = wave_read_lane(incl, kWave - 1);
-      uint32_t wbase = 0;
-      if (lane == kWave - 1 && wtot != 0u) wbase = atomicAdd(&ncand, wtot);
-      wbase = wave_read_lane(wbase, kWave - 1);
-      uint32_t p = wbase + incl - mine;
-      visit_regs([&](uint32_t kk) {
-        if ((kk >> S1) == top) cand[p++] = kk;
-      });
-      block_sync_lds();
-      const uint32_t n_c = cnt;
+  // Rows of up to 16 values per thread search by value bins first; longer
+  // register rows (32 per thread) have no registers to spare for it and go
+  // straight to the radix passes.
+  if constexpr (V <= 16) {
+  // Stage 1: the row's finite min and max and whether it holds a non-finite
+  // value (block reduction); the histogram is cleared meanwhile.
+  constexpr int NW = NT / kWave;
+  const int wid = tid / kWave;
+  constexpr int NBV = 512;  // value bins
+  for (int b = tid; b < NBV / 4; b += NT) reinterpret_cast<uint4*>(hist)[b] = make_uint4(0u, 0u, 0u, 0u);
+  // min/max ignore NaN; +-inf enter them.  NaN and +inf are flagged with
+  // one compare per value; a -inf shows as lo = -inf.
+  float lo = __builtin_huge_valf(), hi = -__builtin_huge_valf();
+  uint64_t spm = 0;
+  visit_vals([&](float x, int) {
+    lo = fminf(lo, x);
+    hi = fmaxf(hi, x);
+    spm |= ballot(!(x < __builtin_huge_valf()));
+  });
+  auto block_range = [&](bool flag) __attribute__((always_inline)) {
+    lo = wave_extreme_f32<false>(lo);
+    hi = wave_extreme_f32<true>(hi);
+    if (lane == 0) {
+      red[wid] = lo;
+      red[NW + wid] = hi;
+      red[2 * NW + wid] = flag ? 1.0f : 0.0f;
+    }
+    block_sync_lds();
+    bool any = false;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      lo = fminf(lo, red[w]);
+      hi = fmaxf(hi, red[NW + w]);
+      any = any || red[2 * NW + w] != 0.0f;
+    }
+    return any;
+  };
+  bool special = block_range(spm != 0u);
+  special = special || !(lo > -__builtin_huge_valf());
+  if (special) {
+    // +-inf or NaN present (block-uniform): the finite range, again.
+    block_sync_lds();  // every wave has read red
+    lo = __builtin_huge_valf();
+    hi = -__builtin_huge_valf();
+    visit_vals([&](float x, int) {
+      const bool fin = fabsf(x) <= __FLT_MAX__;
+      lo = fminf(lo, fin ? x : __builtin_huge_valf());
+      hi = fmaxf(hi, fin ? x : -__builtin_huge_valf());
+    });
+    block_range(false);
+  }
+  // Stage 2: NBV bins linear in value between lo and hi (-inf in the
+  // lowest, +inf and NaN in the highest; a degenerate range puts every finite
+  // value in bin 0).  Bins follow the data's density, so the histogram's
+  // ds_adds rarely collide, and the bin holding the k-th largest usually
+  // holds a few values.  Bins only steer the search: the candidates are
+  // ranked by key, so the result is exact for any input.  Each value's bin
+  // is kept, two per register, for the compaction.
+  constexpr float kTop = static_cast<float>(NBV - 1);
+  // A degenerate range (one finite value, none, or a span that overflows)
+  // keeps scale = 1: every value then falls in the end bins, which only
+  // costs the fallback below.  scale > 0 always, so -inf lands in bin 0.
+  float scale = static_cast<float>(NBV) / (hi - lo);
+  if (!(hi > lo) || !(scale > 0.0f && scale <= __FLT_MAX__)) {
+    scale = 1.0f;
+    if (!(fabsf(lo) <= __FLT_MAX__)) lo = 0.0f;
+  }
+  // x*scale - lo*scale in one rounding: monotone in x, like (x - lo)*scale
+  const float off = -lo * scale;
+  auto bin_of = [&](float x) __attribute__((always_inline)) -> int {
+    int b = static_cast<int>(__builtin_amdgcn_fmed3f(__builtin_fmaf(x, scale, off), 0.0f, kTop));
+    if (special) b = (x != x || x == __builtin_huge_valf()) ? NBV - 1 : b;
+    return b;
+  };
+  uint32_t bp[V / 2];
+#pragma unroll
+  for (int i = 0; i < V / 2; ++i) bp[i] = 0u;
+  visit_vals([&](float x, int i) {
+    const uint32_t b = static_cast<uint32_t>(bin_of(x));
+    atomicAdd(&hist[b], 1u);
+    bp[i >> 1] |= b << (16 * (i & 1));
+  });
+  auto bin_at = [&](int i) __attribute__((always_inline)) {
+    return (bp[i >> 1] >> (16 * (i & 1))) & 0xffffu;
+  };
+  block_sync_lds();
+  find_digit<NT, NBV>(hist, static_cast<uint32_t>(k), wsum, info);
+  const uint32_t bsel = info[0], brank = info[1], bcnt = info[2];
+  if (bcnt <= static_cast<uint32_t>(CAP)) {
+    // Stage 3: the chosen bin's values (a few, usually), as keys, appended
+    // to an LDS list in any order, then ranked by one wave: pairwise when
+    // they fit a wave, else 8-bit radix passes.
+    visit_vals([&](float x, int i) {
+      if (bin_at(i) == bsel) cand[atomicAdd(&ncand, 1u)] = float_to_key(x);
+    });
+    block_sync_lds();
+    // Threshold only: the other waves exit now, so their registers take the
+    // next rows' loads.
+    if (a.idx == nullptr && tid >= kWave) return;
+    if (tid < kWave) {
+      uint32_t tk, ngt;
+      if (bcnt <= static_cast<uint32_t>(kWave)) {
+        const uint32_t mk = lane < static_cast<int>(bcnt) ? cand[lane] : 0u;
+        uint32_t gt = 0, ge = 0;
+        for (uint32_t j = 0; j < bcnt; ++j) {
+          const uint32_t o = cand[j];
+          gt += (o > mk) ? 1u : 0u;
+          ge += (o >= mk) ? 1u : 0u;
+        }
+        const bool hit = lane < static_cast<int>(bcnt) && gt < brank && ge >= brank;
+        const int src = __ffsll(static_cast<unsigned long long>(ballot(hit))) - 1;
+        tk = wave_read_lane(mk, src);
+        ngt = wave_read_lane(gt, src);
+      } else {
+        tk = wave_select_cand(cand, bcnt, 0u, 32, brank, hist);
+        uint32_t g = 0;
+        for (uint32_t i = lane; i < bcnt; i += kWave) g += (cand[i] > tk) ? 1u : 0u;
+        ngt = wave_read_lane(wave_inclusive_sum(g), kWave - 1);
+      }
       if (a.idx == nullptr) {
-        // Threshold only: one wave finishes on the candidates; the other
-        // waves exit now, so their registers take the next rows' loads.
-        if (tid >= kWave) return;
-        const uint32_t tk = wave_select_cand(cand, n_c, prefix, S1, krem, hist);
         if (tid == 0) a.thr[row] = key_to_float(tk);
         return;
       }
-      auto visit_cand = [&](auto&& f) {
-        for (uint32_t i = tid; i < n_c; i += NT) f(cand[i]);
-      };
-      found = radix_pass<NT, S2, B2>(visit_cand, hist, wsum, info, prefix, krem, cnt, true,
-                                     thr_key);
-      if (!found) radix_pass<NT, 0, B3>(visit_cand, hist, wsum, info, prefix, krem, cnt, false,
-                                        thr_key);
-    } else {
-      found = radix_pass<NT, S2, B2>(visit_regs, hist, wsum, info, prefix, krem, cnt, true,
-                                     thr_key);
-      if (!found) radix_pass<NT, 0, B3>(visit_regs, hist, wsum, info, prefix, krem, cnt, false,
-                                        thr_key);
+      if (tid == 0) {
+        info[0] = tk;
+        info[1] = brank - ngt;  // rank of the wanted key among the keys equal to it
+      }
     }
-    if (!found) thr_key = prefix;
+    block_sync_lds();
+    thr_key = info[0];
+    krem = info[1];
+    done = true;
+  }
+  }  // V <= 16
+  if (!done) {
+    // A bin of more than CAP values (heavy ties, or a row whose values
+    // sit at the ends of a huge range), or rows of 32 values per thread: MSD
+    // radix passes over the keys in registers, 11/11/10 (or 12/10/10) bits.
+    to_keys();
+    keys_in_regs = true;
+    // The first pass tests for kKeyNone only in the chunk the row ends inside.
+    auto visit_first = [&](auto&& f) {
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        if (j < nch) {
+          if ((j + 1) * NT * 4 <= nvalid) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) f(key[4 * j + c]);
+          } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              if (key[4 * j + c] != kKeyNone) f(key[4 * j + c]);
+          }
+        }
+      }
+    };
+    uint32_t prefix = 0, cnt = 0;
+    krem = static_cast<uint32_t>(k);
+    bool found = radix_pass<NT, S1, P1, true>(visit_first, hist, wsum, info, prefix, krem, cnt,
+                                              true, thr_key);
+    if (!found) {
+      if (cnt <= static_cast<uint32_t>(CAP)) {
+        const uint32_t top = prefix;
+        uint32_t mine = 0;
+        visit_regs([&](uint32_t kk) { mine += ((kk >> S1) == top) ? 1u : 0u; });
+        const uint32_t incl = wave_inclusive_sum(mine);
+        const uint32_t wtot = wave_read_lane(incl, kWave - 1);
+        uint32_t wbase = 0;
+        if (lane == kWave - 1 && wtot != 0u) wbase = atomicAdd(&ncand, wtot);
+        wbase = wave_read_lane(wbase, kWave - 1);
+        uint32_t p = wbase + incl - mine;
+        visit_regs([&](uint32_t kk) {
+          if ((kk >> S1) == top) cand[p++] = kk;
+        });
+        block_sync_lds();
+        const uint32_t n_c = cnt;
+        if (a.idx == nullptr) {
+          if (tid >= kWave) return;
+          const uint32_t tk = wave_select_cand(cand, n_c, prefix, S1, krem, hist);
+          if (tid == 0) a.thr[row] = key_to_float(tk);
+          return;
+        }
+        auto visit_cand = [&](auto&& f) {
+          for (uint32_t i = tid; i < n_c; i += NT) f(cand[i]);
+        };
+        found = radix_pass<NT, S2, B2>(visit_cand, hist, wsum, info, prefix, krem, cnt, true,
+                                       thr_key);
+        if (!found) radix_pass<NT, 0, B3>(visit_cand, hist, wsum, info, prefix, krem, cnt, false,
+                                          thr_key);
+      } else {
+        found = radix_pass<NT, S2, B2>(visit_regs, hist, wsum, info, prefix, krem, cnt, true,
+                                       thr_key);
+        if (!found) radix_pass<NT, 0, B3>(visit_regs, hist, wsum, info, prefix, krem, cnt, false,
+                                          thr_key);
+      }
+      if (!found) thr_key = prefix;
+    }
   }
   if (tid == 0) a.thr[row] = key_to_float(thr_key);
 
   if (a.idx != nullptr) {
+    if (!keys_in_regs) to_keys();
     int32_t* out = a.idx + row * static_cast<int64_t>(k);
     emit_indices<NT>(out, nch, thr_key, krem, wsum, [&](int64_t j, uint32_t(&kk)[4]) {
 #pragma unroll
@@ -489,6 +662,7 @@ __global__ __launch_bounds__(NT, (V <= 32 && NT <= 512) ? 8 : 4) void topk_reg_k
     });
   }
 }
+
 
 // ---------------------------------------------------------------------------
 // Streaming kernel: any row length; the row is re-read on every pass.
