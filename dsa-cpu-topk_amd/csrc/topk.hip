@@ -16,7 +16,7 @@
 // ranked by key in one wave.  Bins follow the data's density, so the
 // histogram's LDS atomics rarely collide and the finish has a few values to
 // rank; this takes fewer VALU instructions per value than the digit passes
-// below (config 3's causal rows of 1..4096: 44 -> 38 us).  A bin of more than
+// below (config 3's causal rows of 1..4096: 44 -> 35.5 us).  A bin of more than
 // kCandCap values (heavy ties) and longer register rows take MSD radix passes
 // over order-preserving keys, 11/11/10-bit digits:
 //   pass 1  histogram of key[31:21] in LDS (ds_add), block suffix-scan picks
@@ -57,7 +57,22 @@ struct SelectArgs {
   int64_t causal_T;
   float* thr;
   int32_t* idx;
+  int64_t nbatch;  // rows / causal_T in causal mode (set by the host)
 };
+
+// Row r of the 1-D causal order: q = r / nb (rows longest first), r % nb
+// the batch element; 32-bit arithmetic when the grid allows it (r is
+// wave-uniform, so this is scalar work).
+__device__ __forceinline__ void causal_div(int64_t r, int64_t nb, int64_t& q, int64_t& m) {
+  if (r <= 0xffffffffll && nb <= 0xffffffffll) {
+    const uint32_t q32 = static_cast<uint32_t>(r) / static_cast<uint32_t>(nb);
+    q = q32;
+    m = static_cast<uint32_t>(r) - q32 * static_cast<uint32_t>(nb);
+  } else {
+    q = r / nb;
+    m = r % nb;
+  }
+}
 
 
 // Digits of the streaming kernel: key[31:21], key[20:10], key[9:0].
@@ -71,11 +86,17 @@ constexpr int kCandCap = 2048;
 
 __device__ __forceinline__ void row_of_block(const SelectArgs& a, int64_t& row,
                                              int64_t& nvalid) {
-  if (a.causal_T > 0) {
-    const int64_t nb = a.rows / a.causal_T;
-    const int64_t i = blockIdx.x;
-    const int64_t t = a.causal_T - 1 - i / nb;
-    row = (i % nb) * a.causal_T + t;
+  if (a.causal_T > 0 && gridDim.y > 1) {
+    // 2-D causal grid (batch element fastest, then rows longest first): the
+    // same order as the 1-D mapping below, without a 64-bit division.
+    const int64_t t = a.causal_T - 1 - static_cast<int64_t>(blockIdx.y);
+    row = static_cast<int64_t>(blockIdx.x) * a.causal_T + t;
+    nvalid = t + 1;
+  } else if (a.causal_T > 0) {
+    int64_t q, m;
+    causal_div(blockIdx.x, a.nbatch, q, m);
+    const int64_t t = a.causal_T - 1 - q;
+    row = m * a.causal_T + t;
     nvalid = t + 1;
   } else {
     row = blockIdx.x;
@@ -105,8 +126,9 @@ __device__ __forceinline__ bool in_prefix(uint32_t kk, uint32_t prefix) {
 // (one suffix scan for all R ranks).  Thread tid owns bins [tid*BPT,
 // tid*BPT+BPT).  Ends with a barrier after which, for each q, info[3q] =
 // digit, info[3q+1] = rank of the wanted key inside the digit, info[3q+2] =
-// keys in the digit.
-template <int NT, int NB, int R>
+// keys in the digit.  REV: the histogram is stored highest digit first
+// (hist[NB-1-d] counts digit d).
+template <int NT, int NB, int R, bool REV = false>
 __device__ __forceinline__ void find_digits(const uint32_t* hist, const uint32_t (&r)[R],
                                             uint32_t* wsum, uint32_t* info) {
   constexpr int BPT = NB >= NT ? NB / NT : 1;
@@ -118,7 +140,7 @@ __device__ __forceinline__ void find_digits(const uint32_t* hist, const uint32_t
   uint32_t local = 0;
 #pragma unroll
   for (int i = 0; i < BPT; ++i) {
-    h[i] = (lo + i < NB) ? hist[lo + i] : 0u;
+    h[i] = (lo + i < NB) ? hist[REV ? NB - 1 - (lo + i) : lo + i] : 0u;
     local += h[i];
   }
   const uint32_t incl = wave_inclusive_sum(local);
@@ -153,11 +175,11 @@ __device__ __forceinline__ void find_digits(const uint32_t* hist, const uint32_t
   block_sync_lds();
 }
 
-template <int NT, int NB>
+template <int NT, int NB, bool REV = false>
 __device__ __forceinline__ void find_digit(const uint32_t* hist, uint32_t krem, uint32_t* wsum,
                                            uint32_t* info) {
   const uint32_t r[1] = {krem};
-  find_digits<NT, NB, 1>(hist, r, wsum, info);
+  find_digits<NT, NB, 1, REV>(hist, r, wsum, info);
 }
 
 // One radix pass over the keys `visit` enumerates (keys equal to kKeyNone
@@ -453,43 +475,34 @@ __global__ __launch_bounds__(NT, (V <= 32 && NT <= 512) ? 8 : 4) void topk_reg_k
   // register rows (32 per thread) have no registers to spare for it and go
   // straight to the radix passes.
   if constexpr (V <= 16) {
-  // Stage 1: the row's finite min and max and whether it holds a non-finite
-  // value (block reduction); the histogram is cleared meanwhile.
+  // Stage 1: the row's min and max (block reduction; min and max ignore NaN);
+  // the histogram is cleared meanwhile.
   constexpr int NW = NT / kWave;
   const int wid = tid / kWave;
   constexpr int NBV = 512;  // value bins
   for (int b = tid; b < NBV / 4; b += NT) reinterpret_cast<uint4*>(hist)[b] = make_uint4(0u, 0u, 0u, 0u);
-  // min/max ignore NaN; +-inf enter them.  NaN and +inf are flagged with
-  // one compare per value; a -inf shows as lo = -inf.
   float lo = __builtin_huge_valf(), hi = -__builtin_huge_valf();
-  uint64_t spm = 0;
   visit_vals([&](float x, int) {
     lo = fminf(lo, x);
     hi = fmaxf(hi, x);
-    spm |= ballot(!(x < __builtin_huge_valf()));
   });
-  auto block_range = [&](bool flag) __attribute__((always_inline)) {
+  auto block_range = [&]() __attribute__((always_inline)) {
     lo = wave_extreme_f32<false>(lo);
     hi = wave_extreme_f32<true>(hi);
     if (lane == 0) {
       red[wid] = lo;
       red[NW + wid] = hi;
-      red[2 * NW + wid] = flag ? 1.0f : 0.0f;
     }
     block_sync_lds();
-    bool any = false;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       lo = fminf(lo, red[w]);
       hi = fmaxf(hi, red[NW + w]);
-      any = any || red[2 * NW + w] != 0.0f;
     }
-    return any;
   };
-  bool special = block_range(spm != 0u);
-  special = special || !(lo > -__builtin_huge_valf());
-  if (special) {
-    // +-inf or NaN present (block-uniform): the finite range, again.
+  block_range();
+  if (!(lo > -__builtin_huge_valf()) || !(hi < __builtin_huge_valf())) {
+    // An infinite value (block-uniform, rare): the finite range instead.
     block_sync_lds();  // every wave has read red
     lo = __builtin_huge_valf();
     hi = -__builtin_huge_valf();
@@ -498,51 +511,52 @@ __global__ __launch_bounds__(NT, (V <= 32 && NT <= 512) ? 8 : 4) void topk_reg_k
       lo = fminf(lo, fin ? x : __builtin_huge_valf());
       hi = fmaxf(hi, fin ? x : -__builtin_huge_valf());
     });
-    block_range(false);
+    block_range();
   }
-  // Stage 2: NBV bins linear in value between lo and hi (-inf in the
-  // lowest, +inf and NaN in the highest; a degenerate range puts every finite
-  // value in bin 0).  Bins follow the data's density, so the histogram's
-  // ds_adds rarely collide, and the bin holding the k-th largest usually
-  // holds a few values.  Bins only steer the search: the candidates are
-  // ranked by key, so the result is exact for any input.  Each value's bin
-  // is kept, two per register, for the compaction.
+  // Stage 2: NBV bins linear in value between lo and hi.  Bins follow the
+  // data's density, so the histogram's ds_adds rarely collide, and the bin
+  // holding the k-th largest usually holds a few values.  Bins only steer
+  // the search: the candidates are ranked by key, so the result is exact for
+  // any input.  Bins are counted from the top: c = med3((hi - x)*scale, 0,
+  // top) is monotone (decreasing) in the key order with no test for special
+  // values -- +inf lands in c = 0, and NaN too (med3 with a NaN operand
+  // returns the minimum of the other two, 0, and so does the conversion of a
+  // NaN); -inf in c = top.  A degenerate range (one finite value, none, or a
+  // span that overflows) keeps scale = 1: the values then crowd the end
+  // bins, which only costs the fallback below.  Each value's c is kept, two
+  // per register, for the compaction.
   constexpr float kTop = static_cast<float>(NBV - 1);
-  // A degenerate range (one finite value, none, or a span that overflows)
-  // keeps scale = 1: every value then falls in the end bins, which only
-  // costs the fallback below.  scale > 0 always, so -inf lands in bin 0.
   float scale = static_cast<float>(NBV) / (hi - lo);
   if (!(hi > lo) || !(scale > 0.0f && scale <= __FLT_MAX__)) {
     scale = 1.0f;
-    if (!(fabsf(lo) <= __FLT_MAX__)) lo = 0.0f;
+    if (!(fabsf(hi) <= __FLT_MAX__)) hi = 0.0f;
   }
-  // x*scale - lo*scale in one rounding: monotone in x, like (x - lo)*scale
-  const float off = -lo * scale;
-  auto bin_of = [&](float x) __attribute__((always_inline)) -> int {
-    int b = static_cast<int>(__builtin_amdgcn_fmed3f(__builtin_fmaf(x, scale, off), 0.0f, kTop));
-    if (special) b = (x != x || x == __builtin_huge_valf()) ? NBV - 1 : b;
-    return b;
+  // (hi - x)*scale in one rounding: monotone in x
+  const float hoff = hi * scale;
+  auto bin_of = [&](float x) __attribute__((always_inline)) -> uint32_t {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_fmed3f(__builtin_fmaf(x, -scale, hoff), 0.0f, kTop));
   };
   uint32_t bp[V / 2];
 #pragma unroll
   for (int i = 0; i < V / 2; ++i) bp[i] = 0u;
   visit_vals([&](float x, int i) {
-    const uint32_t b = static_cast<uint32_t>(bin_of(x));
-    atomicAdd(&hist[b], 1u);
-    bp[i >> 1] |= b << (16 * (i & 1));
+    const uint32_t c = bin_of(x);
+    atomicAdd(&hist[c], 1u);
+    bp[i >> 1] |= c << (16 * (i & 1));
   });
   auto bin_at = [&](int i) __attribute__((always_inline)) {
     return (bp[i >> 1] >> (16 * (i & 1))) & 0xffffu;
   };
   block_sync_lds();
-  find_digit<NT, NBV>(hist, static_cast<uint32_t>(k), wsum, info);
-  const uint32_t bsel = info[0], brank = info[1], bcnt = info[2];
+  find_digit<NT, NBV, true>(hist, static_cast<uint32_t>(k), wsum, info);
+  const uint32_t csel = NBV - 1 - info[0], brank = info[1], bcnt = info[2];
   if (bcnt <= static_cast<uint32_t>(CAP)) {
     // Stage 3: the chosen bin's values (a few, usually), as keys, appended
     // to an LDS list in any order, then ranked by one wave: pairwise when
     // they fit a wave, else 8-bit radix passes.
     visit_vals([&](float x, int i) {
-      if (bin_at(i) == bsel) cand[atomicAdd(&ncand, 1u)] = float_to_key(x);
+      if (bin_at(i) == csel) cand[atomicAdd(&ncand, 1u)] = float_to_key(x);
     });
     block_sync_lds();
     // Threshold only: the other waves exit now, so their registers take the
@@ -1213,15 +1227,16 @@ __global__ __launch_bounds__(256, V <= 16 ? 8 : (V <= 32 ? 6 : 4)) void topk_wav
   constexpr int NCH = V / 4;  // float4 chunks per lane; chunk j covers 256 entries
   __shared__ __align__(16) uint32_t whist[4][256];
   __shared__ uint32_t wgl[4][kWave];
-  const int wid = threadIdx.x / kWave;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // uniform per wave
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t rid = static_cast<int64_t>(blockIdx.x) * 4 + wid;
   if (rid >= a.rows) return;  // no block-level synchronisation below
   int64_t row, nvalid;
   if (a.causal_T > 0) {  // longest rows first
-    const int64_t nb = a.rows / a.causal_T;
-    const int64_t t = a.causal_T - 1 - rid / nb;
-    row = (rid % nb) * a.causal_T + t;
+    int64_t q, r;
+    causal_div(rid, a.nbatch, q, r);
+    const int64_t t = a.causal_T - 1 - q;
+    row = r * a.causal_T + t;
     nvalid = t + 1;
   } else {
     row = rid;
@@ -1408,7 +1423,13 @@ hipError_t launch_wave(const SelectArgs& a, hipStream_t stream) {
 
 template <int NT, int V, int P1>
 hipError_t launch_reg(const SelectArgs& a, bool vec, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(a.rows));
+  // Causal rows: a 2-D grid (batch element, row) whose blocks need no
+  // division to find their row (register rows are at most 32768 long, so
+  // causal_T fits the grid's y range).
+  const int64_t nb = a.nbatch;
+  const bool two_d = a.causal_T > 1 && a.causal_T <= 65535 && nb <= 0x7fffffff;
+  const dim3 grid = two_d ? dim3(static_cast<unsigned>(nb), static_cast<unsigned>(a.causal_T))
+                          : dim3(static_cast<unsigned>(a.rows));
   if (vec)
     hipLaunchKernelGGL((topk_reg_kernel<NT, V, P1, true>), grid, dim3(NT), 0, stream, a);
   else
@@ -1452,7 +1473,7 @@ hipError_t launch_stream(const SelectArgs& a, bool vec, hipStream_t stream) {
 hipError_t launch_topk(const float* scores, int64_t rows, int64_t n, int64_t ld, int k,
                        int64_t causal_T, float* thr, int32_t* idx, hipStream_t stream) {
   if (rows == 0) return hipSuccess;
-  SelectArgs a{scores, rows, n, ld, k, causal_T, thr, idx};
+  SelectArgs a{scores, rows, n, ld, k, causal_T, thr, idx, causal_T > 0 ? rows / causal_T : 0};
   const int64_t cap = causal_T > 0 ? (causal_T < n ? causal_T : n) : n;
   // float4 loads stay inside [0, n) of every row only when n, ld and the base
   // are all 16-byte granular.
