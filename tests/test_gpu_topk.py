@@ -92,6 +92,68 @@ def test_nan_inf_rows_threshold_only(dev, n):
                                    rtol=0, atol=0, equal_nan=True, msg=f"n={n} k={k}")
 
 
+def nonfinite_rows(n, seed):
+    """Rows of n entries with NaN, +-inf, heavy ties, +-0, denormals and a
+    span that overflows (the cases the value bins of the register kernel
+    must order exactly as keys do)."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((8, n), generator=g)
+    x[0, ::7] = float("nan")
+    x[1, ::5] = float("inf")
+    x[1, 1::5] = float("-inf")
+    x[2] = torch.where(torch.rand(n, generator=g) < 0.5, 1.0, float("nan"))
+    x[3] = torch.randint(0, 3, (n,), generator=g).float()
+    x[3, 17] = float("nan")
+    x[4] = float("-inf")
+    x[4, 3] = 0.0
+    x[5] = torch.where(torch.rand(n, generator=g) < 0.5, 0.0, -0.0)
+    x[6] = x[6] * 1e-42
+    x[7, :] = 3.0e38
+    x[7, ::3] = -3.0e38
+    return x
+
+
+@pytest.mark.parametrize("n", [1000, 4096])
+def test_nan_inf_rows_with_indices(dev, n):
+    """Thresholds with exactly-k indices on rows with non-finite values
+    (block kernel: value bins, NaN counted in the top bin and ranked first
+    by key); index sets bit-exact against the stable descending sort."""
+    x = nonfinite_rows(n, n + 1)
+    xg = x.to(dev)
+    for k in sorted({1, 7, n // 3, n - 1, n}):
+        say(f"topk indices nan/inf n={n} k={k}")
+        thr, idx = topk_indices(xg, k)
+        torch.testing.assert_close(thr.cpu(), O.topk_threshold(x, k), rtol=0, atol=0,
+                                   equal_nan=True, msg=f"n={n} k={k}")
+        want = O.select_indices(x.numpy(), k)
+        bad = np.flatnonzero((idx.cpu().numpy() != want).any(-1).reshape(-1))
+        assert bad.size == 0, f"n={n} k={k}: rows {bad[:4]} differ"
+
+
+def test_causal_nonfinite_rows_2d_grid(dev):
+    """Causal rows of 1..4096 entries (the register kernel's 2-D grid: batch
+    element x row, longest rows first) with non-finite scores in the causal
+    part: thresholds and index sets equal the dense select on rows whose
+    s > t entries are -inf."""
+    B, T, k = 2, 4096, 256
+    s = torch.randn((B, T, T), generator=torch.Generator().manual_seed(3))
+    s[0, :, ::11] = float("nan")
+    s[1, ::2, ::13] = float("inf")
+    s[1, 1::2, 5::7] = float("-inf")
+    dense = s.clone()
+    dense[:, torch.ones(T, T, dtype=torch.bool).triu(1)] = float("-inf")
+    rows = [0, 1, 2, 255, 256, 257, 1000, 2047, 2048, 4094, 4095]
+    sg = s.to(dev)
+    thr_c, idx_c = topk_indices(sg, k, causal=True)
+    thr_t = topk_threshold(sg, k, causal=True)
+    say(f"topk causal nonfinite B={B} T={T} k={k}")
+    want_thr = O.topk_threshold(dense[:, rows], k)
+    torch.testing.assert_close(thr_c[:, rows].cpu(), want_thr, rtol=0, atol=0, equal_nan=True)
+    torch.testing.assert_close(thr_t[:, rows].cpu(), want_thr, rtol=0, atol=0, equal_nan=True)
+    want_idx = O.select_indices(dense[:, rows].numpy(), k)
+    assert np.array_equal(idx_c[:, rows].cpu().numpy(), want_idx)
+
+
 def test_bracket_path_misses_fall_back(dev):
     """Threshold-only rows above 4096 entries are selected in one pass from a
     bracket that an evenly spread 4096-entry sample (chunks 0, 4, 8, 12 of
