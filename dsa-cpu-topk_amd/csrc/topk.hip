@@ -1191,7 +1191,16 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
       }
       if (staged) {
         block_sync_lds();
-        for (int i = tid; i < k; i += NT) out[i] = so[i];
+        // 16-byte stores when the row allows them; streamed past the caches
+        // (the index rows are not re-read by this kernel)
+        typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+        if ((k & 3) == 0 && (reinterpret_cast<uintptr_t>(a.idx) & 15u) == 0u) {
+          const i32x4* s4 = reinterpret_cast<const i32x4*>(so);
+          i32x4* o4 = reinterpret_cast<i32x4*>(out);
+          for (int i = tid; i < k / 4; i += NT) __builtin_nontemporal_store(s4[i], o4 + i);
+        } else {
+          for (int i = tid; i < k; i += NT) out[i] = so[i];
+        }
       }
     }
     return;
