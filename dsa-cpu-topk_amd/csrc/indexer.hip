@@ -11,12 +11,13 @@
 //   fits in LDS).  A block owns TQ = 4*NQ consecutive queries of one batch
 //   element.  It stages their q rows (all heads) into LDS once, already in
 //   MFMA fragment order, so every later A-operand read is one conflict-free
-//   ds_read_b128 per lane, and their w rows next to them.  Its 8 waves then
-//   split the causal key range [0, t0+TQ) into super-blocks of 16*KB keys,
-//   load each super-block's k rows straight into B-operand registers
-//   (prefetching the next), and run all TQ queries x HI heads against it.  q
-//   is read from HBM exactly once; k (B*T*DI elements) is re-read from L2 /
-//   MALL once per query tile.
+//   ds_read_b128 per lane, and their w rows next to them.  Its 16 waves (4
+//   per SIMD: the q tile fills the CU's LDS, so one block is all a CU holds)
+//   then split the causal key range [0, t0+TQ) into super-blocks of 16*KB
+//   keys, load each super-block's k rows straight into B-operand registers,
+//   and run all TQ queries x HI heads against it.  q is read from HBM
+//   exactly once; k (B*T*DI elements) is re-read from L2 / MALL once per
+//   query tile.
 //
 // indexer_kernel (register-streaming; fallback for very wide q rows).  Grid
 //   x = (batch, 16-query tile), y = 256-key chunk; each wave owns 4 queries
@@ -97,7 +98,11 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerArgs a) {
 // ---------------------------------------------------------------------------
 // Query-stationary kernel.
 // ---------------------------------------------------------------------------
-constexpr int kQWaves = 8;
+// 16 waves = 4 per SIMD, which caps a wave at 128 registers: one super-block
+// of B operands (64 for 16-bit DI = 128), no second set to prefetch into --
+// the SIMD's other three waves cover a wave's key-row latency instead.
+// (8 waves with two register sets ping-ponged: config 4 1.68 -> 1.56 ms.)
+constexpr int kQWaves = 16;
 #ifndef DSA_QTILE_MAX_NQ
 #define DSA_QTILE_MAX_NQ 4
 #endif
@@ -255,10 +260,8 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
   constexpr int SB = 16 * KB;
   const int nsb = (t_end + SB - 1) / SB;
 
-  // k rows of super-block sb into B registers.  Rows past T (and whole
-  // super-blocks past the last one, loaded as prefetch) are clamped to row
-  // T-1: their scores are never stored, and unconditional loads keep the
-  // wait counts exact so the prefetch stays in flight during the MFMAs.
+  // k rows of super-block sb into B registers.  Rows past T are clamped to
+  // row T-1: their scores are never stored.
   // k's scales of a super-block: one load per lane (lane l holds key
   // s0 + l % SB), spread to the lanes that store each key by row swaps.
   const float* ksc = KS && a.k_scale != nullptr ? a.k_scale + b * T : nullptr;
@@ -320,6 +323,19 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb) acc[kb] = mfma_fp8<E>(a0, a1, bk[kb], c, acc[kb]);
           }
+        } else if constexpr (Tag::kBytes == 2 && NCH <= 4 && NQ <= 2) {
+          // All of the unit's A fragments read before its MFMAs (a scheduling
+          // fence keeps them together): one LDS latency per unit, not one per
+          // chunk (config 4 1.56 -> 1.51 ms; fp32 is faster without it, and
+          // wider rows or four quads would spill the 128 registers).
+          uint4 av[NCH];
+#pragma unroll
+          for (int c = 0; c < NCH; ++c) av[c] = qa[((qd * nhg + hg) * NCH + c) * 64];
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) acc[kb] = mfma_chunk<Tag, E>(av[c], bk[kb], c, acc[kb]);
         } else {
 #pragma unroll
           for (int c = 0; c < NCH; ++c) {
@@ -356,20 +372,13 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
     }
   };
 
-  // Ping-pong over two register sets: compute on one while the other loads.
-  const int last = nsb - 1;
-  S b0[KB], b1[KB];
-  float k0s = 1.f, k1s = 1.f;  // k's scales (KS only; otherwise unused)
-  int sb = wave;
-  load_b(min(sb, last), b0, k0s);
-  while (sb < nsb) {
-    load_b(min(sb + kQWaves, last), b1, k1s);
-    compute(sb, b0, k0s);
-    sb += kQWaves;
-    if (sb >= nsb) break;
-    load_b(min(sb + kQWaves, last), b0, k0s);
-    compute(sb, b1, k1s);
-    sb += kQWaves;
+  // One register set per wave: a super-block's rows load, then its products
+  // run; the SIMD's other waves issue MFMAs while this one waits on L2.
+  S bk[KB];
+  float ksr = 1.f;  // k's scale (KS only; otherwise unused)
+  for (int sb = wave; sb < nsb; sb += kQWaves) {
+    load_b(sb, bk, ksr);
+    compute(sb, bk, ksr);
   }
 
   // Keys past the last super-block are above the diagonal for every query.
