@@ -108,6 +108,23 @@ __device__ __forceinline__ float wave_extreme_f32(float v) {
   v = op(v, dpp_keep_f32<0x143, 0xc>(v));
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
+// The same for unsigned integers (the wave's least or greatest key).
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_keep_u32(uint32_t v) {
+  const int b = static_cast<int>(v);
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(b, b, CTRL, ROW_MASK, 0xf, false));
+}
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_extreme_u32(uint32_t v) {
+  auto op = [](uint32_t x, uint32_t y) { return MAX ? max(x, y) : min(x, y); };
+  v = op(v, dpp_keep_u32<0x111>(v));
+  v = op(v, dpp_keep_u32<0x112>(v));
+  v = op(v, dpp_keep_u32<0x114>(v));
+  v = op(v, dpp_keep_u32<0x118>(v));
+  v = op(v, dpp_keep_u32<0x142, 0xa>(v));
+  v = op(v, dpp_keep_u32<0x143, 0xc>(v));
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
 
 // DPP lane moves of a float inside 16-lane rows (VALU, no LDS round trip).
 template <int CTRL>

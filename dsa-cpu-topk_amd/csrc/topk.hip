@@ -1222,14 +1222,17 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
 // ---------------------------------------------------------------------------
 // The row is held in registers (V values per lane, float4 loads issued
 // before the first use); no block barrier is involved, so a CU holds many
-// rows at once.  The k-th largest is found as in wave_select_kth_bins: the
-// row's finite min and max (DPP), a 256-bin LDS histogram linear in value
-// between them (-inf in the lowest bin, +inf and NaN in the highest), a
-// suffix scan for the bin holding rank k, then that bin's few values
-// gathered and ranked against each other by key (NaN largest, -0 == +0).  A
-// bin of more than 64 values (heavy ties) takes 8-bit radix passes over its
-// keys instead.  Bins only steer the search: ranking by key makes the result
-// exact for any input.
+// rows at once.  The k-th largest is found from the row's finite min and max
+// (DPP), a 256-bin LDS histogram linear in value between them, counted from
+// the top (+inf and NaN in the first bin, -inf in the last), a prefix scan
+// for the bin holding rank k, then that bin's few values gathered and ranked
+// against each other by key (NaN largest, -0 == +0).  A bin of more than 64
+// values (heavy ties) takes 8-bit radix passes over its keys instead.  Bins
+// only steer the search: ranking by key makes the result exact for any
+// input.  The kernel is bound by instruction issue more than by HBM, so each
+// value costs one min/max, one fma + med3 + convert for its bin (kept, 8 bits
+// each, for the gather) and one LDS add (config 2 standalone: 222 -> 177 us,
+// 60 -> 75% of HBM peak).
 template <int V>
 __global__ __launch_bounds__(256, V <= 16 ? 8 : (V <= 32 ? 6 : 4)) void topk_wave_kernel(
     SelectArgs a) {
@@ -1319,46 +1322,94 @@ __global__ __launch_bounds__(256, V <= 16 ? 8 : (V <= 32 ? 6 : 4)) void topk_wav
     rank = wave_read_lane(rank, src);
     cnt = wave_read_lane(cnt, src);
   };
+  // As pick, for bins counted from the top (bin 0 holds the largest values).
+  auto pick_top = [&](uint32_t want, uint32_t& bin, uint32_t& rank, uint32_t& cnt) {
+    const uint4 h4 = reinterpret_cast<const uint4*>(hist)[lane];
+    const uint32_t h[4] = {h4.x, h4.y, h4.z, h4.w};
+    const uint32_t local = h[0] + h[1] + h[2] + h[3];
+    const uint32_t abv = wave_inclusive_sum(local) - local;  // in lower lanes' bins
+    const bool here = abv < want && abv + local >= want;
+    bin = rank = cnt = 0;
+    if (here) {
+      uint32_t cum = abv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (cnt == 0u && cum + h[i] >= want) {
+          bin = 4u * lane + i;
+          rank = want - cum;
+          cnt = h[i];
+        }
+        cum += h[i];
+      }
+    }
+    const int src = __ffsll(static_cast<unsigned long long>(ballot(here))) - 1;
+    bin = wave_read_lane(bin, src);
+    rank = wave_read_lane(rank, src);
+    cnt = wave_read_lane(cnt, src);
+  };
+  // The row's min and max (fminf / fmaxf ignore NaN); a row holding an
+  // infinite value (wave-uniform, rare) takes its finite range instead.
   float lo = __builtin_huge_valf(), hi = -__builtin_huge_valf();
-  bool special = false;  // +-inf or NaN present
   visit([&](float x, int) {
-    const bool fin = fabsf(x) <= __FLT_MAX__;
-    lo = fminf(lo, fin ? x : __builtin_huge_valf());
-    hi = fmaxf(hi, fin ? x : -__builtin_huge_valf());
-    special = special || !fin;
+    lo = fminf(lo, x);
+    hi = fmaxf(hi, x);
   });
   lo = wave_extreme_f32<false>(lo);
   hi = wave_extreme_f32<true>(hi);
-  special = ballot(special) != 0u;
-  float scale = 255.0f / (hi - lo);
-  if (!(hi > lo) || !(scale <= __FLT_MAX__)) {
-    scale = 0.0f;
-    lo = 0.0f;
+  if (!(lo > -__builtin_huge_valf()) || !(hi < __builtin_huge_valf())) {
+    lo = __builtin_huge_valf();
+    hi = -__builtin_huge_valf();
+    visit([&](float x, int) {
+      const bool fin = fabsf(x) <= __FLT_MAX__;
+      lo = fminf(lo, fin ? x : __builtin_huge_valf());
+      hi = fmaxf(hi, fin ? x : -__builtin_huge_valf());
+    });
+    lo = wave_extreme_f32<false>(lo);
+    hi = wave_extreme_f32<true>(hi);
   }
-  // Monotone in key order: finite values linear in value, -inf in bin 0,
-  // +inf and NaN in bin 255.
-  auto bin_of = [&](float x) -> int {
-    int b = value_bin(x, lo, scale, 255.0f);
-    if (special) {
-      b = (x != x || x == __builtin_huge_valf()) ? 255 : b;
-      b = (x == -__builtin_huge_valf()) ? 0 : b;
-    }
-    return b;
+  // 256 bins linear in value, counted from the top: c = med3((hi - x)*scale,
+  // 0, 255), the product and difference in one rounding (fma), is monotone
+  // (decreasing) in key order with no test for special values -- +inf lands
+  // in c = 0, and so does NaN (med3 with a NaN operand returns the minimum of
+  // the other two, and every NaN is the largest key); -inf in c = 255.  A
+  // degenerate range (one finite value, none, or a span that overflows)
+  // keeps scale = 1: the values then crowd the end bins, which only costs
+  // the heavy-tie path below.  Each value's bin is kept, four per register,
+  // for the gather.
+  float scale = 256.0f / (hi - lo);
+  if (!(hi > lo) || !(scale > 0.0f && scale <= __FLT_MAX__)) {
+    scale = 1.0f;
+    if (!(fabsf(hi) <= __FLT_MAX__)) hi = 0.0f;
+  }
+  const float hoff = hi * scale;
+  auto bin_of = [&](float x) -> uint32_t {
+    return static_cast<uint32_t>(__builtin_amdgcn_fmed3f(__builtin_fmaf(x, -scale, hoff), 0.0f, 255.0f));
   };
   reinterpret_cast<uint4*>(hist)[lane] = make_uint4(0u, 0u, 0u, 0u);
   wave_lds_sync();
-  visit([&](float x, int) { atomicAdd(&hist[bin_of(x)], 1u); });
+  uint32_t bp[V / 4];
+#pragma unroll
+  for (int i = 0; i < V / 4; ++i) bp[i] = 0u;
+  visit([&](float x, int i) {
+    const uint32_t c = bin_of(x);
+    atomicAdd(&hist[c], 1u);
+    bp[i >> 2] |= c << (8 * (i & 3));
+  });
   wave_lds_sync();
   uint32_t bsel, brank, bcnt;
-  pick(static_cast<uint32_t>(k), bsel, brank, bcnt);
+  pick_top(static_cast<uint32_t>(k), bsel, brank, bcnt);
   uint32_t tk;
   if (bcnt <= static_cast<uint32_t>(kWave)) {
+    // The chosen bin's values (a few, usually), as keys, compacted into the
+    // wave's list; register slots where no lane matches cost one compare.
     uint32_t ng = 0;
-    visit([&](float x, int) {
-      const bool in = bin_of(x) == static_cast<int>(bsel);
+    visit([&](float x, int i) {
+      const bool in = ((bp[i >> 2] >> (8 * (i & 3))) & 255u) == bsel;
       const uint64_t m = ballot(in);
-      if (in) gl[ng + lanes_below(m)] = float_to_key(x);
-      ng += popc64(m);
+      if (m != 0u) {
+        if (in) gl[ng + lanes_below(m)] = float_to_key(x);
+        ng += popc64(m);
+      }
     });
     wave_lds_sync();
     const uint32_t mk = lane < static_cast<int>(bcnt) ? gl[lane] : 0u;
@@ -1371,54 +1422,79 @@ __global__ __launch_bounds__(256, V <= 16 ? 8 : (V <= 32 ? 6 : 4)) void topk_wav
     const bool hit = lane < static_cast<int>(bcnt) && gt < brank && ge >= brank;
     tk = wave_read_lane(mk, __ffsll(static_cast<unsigned long long>(ballot(hit))) - 1);
   } else {
-    // Heavy ties: 8-bit radix passes over the keys of the chosen bin's
-    // entries, tracked as a per-lane bit mask of entry slots.  The passes
-    // re-read the row (from L2: it was just read) instead of keeping its keys
-    // in registers, so this rare path costs the common one no registers.
-    const char* rb = reinterpret_cast<const char*>(a.scores + row * a.ld);
-    const int last4 = (nv - 1) & ~3;
-    auto reload = [&](auto&& f) {  // f(key, slot) for every valid entry
-      for (int j = 0; j < nch; ++j) {
-        const int p0 = (j * kWave + lane) * 4;
-        const uint32_t off = static_cast<uint32_t>(min(p0, last4)) * 4u;
-        const float4 q4 = *reinterpret_cast<const float4*>(rb + off);
-        const float xs[4] = {q4.x, q4.y, q4.z, q4.w};
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          if (p0 + c < nv) f(xs[c], 4 * j + c);
+    // Heavy ties.  Often every value of the chosen bin is the same (the
+    // exact zeros of a score row whose weights are all negative, say): that
+    // value is then the k-th largest, and the bin's least and greatest keys,
+    // from the registers, show it without touching memory.
+    uint32_t kmin = ~0u, kmax = 0u;
+    visit([&](float x, int i) {
+      if (((bp[i >> 2] >> (8 * (i & 3))) & 255u) == bsel) {
+        const uint32_t key = float_to_key(x);
+        kmin = min(kmin, key);
+        kmax = max(kmax, key);
       }
-    };
-    uint64_t cm = 0;
-    reload([&](float x, int i) {
-      if (bin_of(x) == static_cast<int>(bsel)) cm |= uint64_t{1} << i;
     });
-    uint32_t prefix = 0, kr = brank, cnt = 0;
-    int sh = 24;
-    for (; sh >= 0; sh -= 8) {
-      wave_lds_sync();  // previous reads of hist done
-      reinterpret_cast<uint4*>(hist)[lane] = make_uint4(0u, 0u, 0u, 0u);
-      wave_lds_sync();
-      reload([&](float x, int i) {
-        if ((cm >> i) & 1u) atomicAdd(&hist[(float_to_key(x) >> sh) & 255u], 1u);
-      });
-      wave_lds_sync();
-      uint32_t d, knew;
-      pick(kr, d, knew, cnt);
-      reload([&](float x, int i) {
-        if (((float_to_key(x) >> sh) & 255u) != d) cm &= ~(uint64_t{1} << i);
-      });
-      prefix = (prefix << 8) | d;
-      kr = knew;
-      if (cnt == 1u) break;
-    }
-    if (cnt == 1u && sh > 0) {  // one candidate left: its full key
-      uint32_t mine = 0;
-      reload([&](float x, int i) {
-        if ((cm >> i) & 1u) mine = float_to_key(x);
-      });
-      tk = wave_read_lane(mine, __ffsll(static_cast<unsigned long long>(ballot(cm != 0u))) - 1);
+    kmin = wave_extreme_u32<false>(kmin);
+    kmax = wave_extreme_u32<true>(kmax);
+    if (kmin == kmax) {
+      tk = kmin;
     } else {
-      tk = prefix;
+      // Otherwise 8-bit radix passes over the keys of the chosen bin's
+      // entries, tracked as a per-lane bit mask of entry slots.  Rows of up
+      // to 16 values per lane keep their values in registers for them (a
+      // launch of short rows ends with its slowest row, and a pass that
+      // re-reads memory costs an L2 round trip: config 1's select 10.3 ->
+      // 7.3 us); longer rows re-read the row (from L2: it was just read), so
+      // this rare path costs the common one no registers.
+      const char* rb = reinterpret_cast<const char*>(a.scores + row * a.ld);
+      const int last4 = (nv - 1) & ~3;
+      auto reload = [&](auto&& f) {  // f(key, slot) for every valid entry
+        if constexpr (V <= 16) {
+          visit(f);
+          return;
+        }
+        for (int j = 0; j < nch; ++j) {
+          const int p0 = (j * kWave + lane) * 4;
+          const uint32_t off = static_cast<uint32_t>(min(p0, last4)) * 4u;
+          const float4 q4 = *reinterpret_cast<const float4*>(rb + off);
+          const float xs[4] = {q4.x, q4.y, q4.z, q4.w};
+  #pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (p0 + c < nv) f(xs[c], 4 * j + c);
+        }
+      };
+      uint64_t cm = 0;
+      reload([&](float x, int i) {
+        if (bin_of(x) == bsel) cm |= uint64_t{1} << i;
+      });
+      uint32_t prefix = 0, kr = brank, cnt = 0;
+      int sh = 24;
+      for (; sh >= 0; sh -= 8) {
+        wave_lds_sync();  // previous reads of hist done
+        reinterpret_cast<uint4*>(hist)[lane] = make_uint4(0u, 0u, 0u, 0u);
+        wave_lds_sync();
+        reload([&](float x, int i) {
+          if ((cm >> i) & 1u) atomicAdd(&hist[(float_to_key(x) >> sh) & 255u], 1u);
+        });
+        wave_lds_sync();
+        uint32_t d, knew;
+        pick(kr, d, knew, cnt);
+        reload([&](float x, int i) {
+          if (((float_to_key(x) >> sh) & 255u) != d) cm &= ~(uint64_t{1} << i);
+        });
+        prefix = (prefix << 8) | d;
+        kr = knew;
+        if (cnt == 1u) break;
+      }
+      if (cnt == 1u && sh > 0) {  // one candidate left: its full key
+        uint32_t mine = 0;
+        reload([&](float x, int i) {
+          if ((cm >> i) & 1u) mine = float_to_key(x);
+        });
+        tk = wave_read_lane(mine, __ffsll(static_cast<unsigned long long>(ballot(cm != 0u))) - 1);
+      } else {
+        tk = prefix;
+      }
     }
   }
   if (lane == 0) a.thr[row] = key_to_float(tk);
@@ -1494,7 +1570,7 @@ hipError_t launch_topk(const float* scores, int64_t rows, int64_t n, int64_t ld,
   // and the chosen digit leaves half the candidates.
   // Rows above 4K entries: one pass over HBM (bracket kernel);
   // threshold-only rows up to 2K entries: one wave per row, the row in registers (config 2
-  // standalone: 284 -> 224 us; at 4K entries, 64 registers of row per lane
+  // standalone: 284 -> 177 us; at 4K entries, 64 registers of row per lane
   // leave 4 waves per SIMD and the block kernel is faster: 43 vs 45 us).
   // With indices: rows of at most 16 chunks (the per-thread position masks
   // are 64 bits).
