@@ -569,7 +569,7 @@ __global__ __launch_bounds__(NT, (V <= 32 && NT <= 512) ? 8 : 4) void topk_reg_k
         const uint32_t mk = lane < static_cast<int>(bcnt) ? cand[lane] : 0u;
         uint32_t gt = 0, ge = 0;
         for (uint32_t j = 0; j < bcnt; ++j) {
-          const uint32_t o = cand[j];
+          const uint32_t o = wave_read_lane(mk, static_cast<int>(j));  // lane j's key, no LDS read
           gt += (o > mk) ? 1u : 0u;
           ge += (o >= mk) ? 1u : 0u;
         }
@@ -1101,7 +1101,7 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
         const float mv = lane < static_cast<int>(bcnt) ? __uint_as_float(gl[lane]) : 0.0f;
         uint32_t gt = 0, ge = 0;
         for (uint32_t j = 0; j < bcnt; ++j) {
-          const float o = __uint_as_float(gl[j]);
+          const float o = __int_as_float(wave_read_lane(__float_as_int(mv), static_cast<int>(j)));
           gt += (o > mv) ? 1u : 0u;
           ge += (o >= mv) ? 1u : 0u;
         }
@@ -1415,7 +1415,7 @@ __global__ __launch_bounds__(256, V <= 16 ? 8 : (V <= 32 ? 6 : 4)) void topk_wav
     const uint32_t mk = lane < static_cast<int>(bcnt) ? gl[lane] : 0u;
     uint32_t gt = 0, ge = 0;
     for (uint32_t j = 0; j < bcnt; ++j) {
-      const uint32_t o = gl[j];
+      const uint32_t o = wave_read_lane(mk, static_cast<int>(j));  // lane j's key, no LDS read
       gt += (o > mk) ? 1u : 0u;
       ge += (o >= mk) ? 1u : 0u;
     }

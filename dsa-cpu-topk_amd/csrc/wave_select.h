@@ -155,7 +155,7 @@ __device__ __forceinline__ float wave_select_kth_bins(const float* row, int n, i
   const float mv = lane < static_cast<int>(bcnt) ? __uint_as_float(gl[lane]) : 0.0f;
   uint32_t gt = 0, ge = 0;
   for (uint32_t j = 0; j < bcnt; ++j) {
-    const float o = __uint_as_float(gl[j]);
+    const float o = __int_as_float(wave_read_lane(__float_as_int(mv), static_cast<int>(j)));  // no LDS read
     gt += (o > mv) ? 1u : 0u;
     ge += (o >= mv) ? 1u : 0u;
   }
