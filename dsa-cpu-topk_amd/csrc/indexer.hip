@@ -12,7 +12,8 @@
 //   element.  It stages their q rows (all heads) into LDS once, already in
 //   MFMA fragment order, so every later A-operand read is one conflict-free
 //   ds_read_b128 per lane, and their w rows next to them.  Its 16 waves (4
-//   per SIMD: the q tile fills the CU's LDS, so one block is all a CU holds)
+//   per SIMD: the q tile fills the CU's LDS, so one block is all a CU holds;
+//   8 for fp8 at DI <= 64)
 //   then split the causal key range [0, t0+TQ) into super-blocks of 16*KB
 //   keys, load each super-block's k rows straight into B-operand registers,
 //   and run all TQ queries x HI heads against it.  q is read from HBM
@@ -98,11 +99,15 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerArgs a) {
 // ---------------------------------------------------------------------------
 // Query-stationary kernel.
 // ---------------------------------------------------------------------------
-// 16 waves = 4 per SIMD, which caps a wave at 128 registers: one super-block
-// of B operands (64 for 16-bit DI = 128), no second set to prefetch into --
-// the SIMD's other three waves cover a wave's key-row latency instead.
-// (8 waves with two register sets ping-ponged: config 4 1.68 -> 1.56 ms.)
-constexpr int kQWaves = 16;
+// Waves per block.  16 = 4 per SIMD, which caps a wave at 128 registers: one
+// super-block of B operands (64 for 16-bit DI = 128), no second set to
+// prefetch into -- the SIMD's other three waves cover a wave's key-row
+// latency instead (8 waves with two register sets ping-ponged: config 4
+// 1.68 -> 1.56 ms; fp8 1.0 -> 0.89 ms at DI = 128).  fp8 at DI <= 64 does
+// half-padded MFMAs on 16-register operand sets, and there 8 waves with the
+// ping-pong stay faster (0.76 vs 0.80 ms at T = 16384, HI = 64).
+template <typename Tag, int DI, int NQ>
+constexpr int qtile_waves() { return (__is_same(Tag, FP8) && DI <= 64) ? 8 : 16; }
 #ifndef DSA_QTILE_MAX_NQ
 #define DSA_QTILE_MAX_NQ 4
 #endif
@@ -193,7 +198,9 @@ size_t qtile_lds_bytes(QTileShape sh) {
 // so q's scale is folded into w when w is staged and k's multiplies each
 // finished score (loaded with the key block it belongs to).
 template <typename Tag, int DI, int KB, int NQ, bool KS = false>
-__global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs a) {
+__global__ __launch_bounds__((64 * qtile_waves<Tag, DI, NQ>())) void indexer_qtile_kernel(
+    IndexerArgs a) {
+  constexpr int NW = qtile_waves<Tag, DI, NQ>();
   using raw = typename Tag::raw;
   using S = Slice<Tag, DI / 4>;
   constexpr int NCH = lane_chunks<Tag, DI>();
@@ -228,7 +235,7 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
     const int hp4 = 4 * nhg;
     const int per_t = hp4 * (DI / EPC);
     const int total = TQ * per_t;
-    for (int u = tid; u < total; u += 64 * kQWaves) {
+    for (int u = tid; u < total; u += 64 * NW) {
       const int tl = u / per_t;
       const int rem = u - tl * per_t;
       const int h = rem / (DI / EPC);
@@ -242,7 +249,7 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
       const int ln = gg * 16 + 4 * (tl & 3) + (h & 3);
       qf[((static_cast<size_t>(tl >> 2) * nhg + (h >> 2)) * NCH + c) * 64 + ln] = v;
     }
-    for (int u = tid; u < TQ * hp4; u += 64 * kQWaves) {
+    for (int u = tid; u < TQ * hp4; u += 64 * NW) {
       const int tl = u / hp4;
       const int h = u - tl * hp4;
       const int t = t0 + tl;
@@ -372,13 +379,35 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
     }
   };
 
-  // One register set per wave: a super-block's rows load, then its products
-  // run; the SIMD's other waves issue MFMAs while this one waits on L2.
-  S bk[KB];
-  float ksr = 1.f;  // k's scale (KS only; otherwise unused)
-  for (int sb = wave; sb < nsb; sb += kQWaves) {
-    load_b(sb, bk, ksr);
-    compute(sb, bk, ksr);
+  if constexpr (NW == 16) {
+    // One register set per wave: a super-block's rows load, then its
+    // products run; the SIMD's other waves issue MFMAs while this one waits
+    // on L2.
+    S bk[KB];
+    float ksr = 1.f;  // k's scale (KS only; otherwise unused)
+    for (int sb = wave; sb < nsb; sb += NW) {
+      load_b(sb, bk, ksr);
+      compute(sb, bk, ksr);
+    }
+  } else {
+    // Two register sets ping-pong: the next super-block's rows load during
+    // this one's products.  Super-blocks past the last one load row T-1's
+    // clamp like rows past T (never stored); unconditional loads keep the
+    // wait counts exact, so the prefetch stays in flight during the MFMAs.
+    const int last = nsb - 1;
+    S b0[KB], b1[KB];
+    float k0s = 1.f, k1s = 1.f;  // k's scales (KS only; otherwise unused)
+    int sb = wave;
+    load_b(min(sb, last), b0, k0s);
+    while (sb < nsb) {
+      load_b(min(sb + NW, last), b1, k1s);
+      compute(sb, b0, k0s);
+      sb += NW;
+      if (sb >= nsb) break;
+      load_b(min(sb + NW, last), b0, k0s);
+      compute(sb, b1, k1s);
+      sb += NW;
+    }
   }
 
   // Keys past the last super-block are above the diagonal for every query.
@@ -386,7 +415,7 @@ __global__ __launch_bounds__(64 * kQWaves) void indexer_qtile_kernel(IndexerArgs
     const int s_lo = nsb * SB;
     const int width = T - s_lo;
     if (width > 0) {
-      for (int tl = wave; tl < TQ; tl += kQWaves) {
+      for (int tl = wave; tl < TQ; tl += NW) {
         const int t = t0 + tl;
         if (t >= T) break;
         for (int s = s_lo + lane; s < T; s += 64) out[static_cast<int64_t>(t) * a.ld + s] = ninf;
@@ -408,7 +437,7 @@ hipError_t launch_qtile(const IndexerArgs& a, QTileShape sh, hipStream_t stream)
   }();
   (void)attr_set;
   const int64_t nblk = a.B * ((a.T + 4 * NQ - 1) / (4 * NQ));
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(nblk)), dim3(64 * kQWaves), lds, stream,
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(nblk)), dim3(64 * qtile_waves<Tag, DI, NQ>()), lds, stream,
                      a);
   return hipGetLastError();
 }
