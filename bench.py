@@ -455,6 +455,7 @@ def bench_select_c4(dev, reps=20):
     stream = torch.cuda.current_stream(dev)
     warm(lambda: topk_threshold(scores, k, causal=True))
     t_thr = time_events(lambda: topk_threshold(scores, k, causal=True), reps, stream)
+    warm(lambda: topk_indices(scores, k, causal=True))
     t_idx = time_events(lambda: topk_indices(scores, k, causal=True), reps, stream)
     read = 4.0 * T * (T + 1) / 2
     out_thr = 4.0 * T
