@@ -205,9 +205,10 @@ def bench_split_long(dev, cfg, dtype, name, reps, fp8_indexer=False):
     timed with HIP events on the stream it runs on."""
     import torch
 
-    from dsa_attention import sparse_attention_hip
+    import _dsa_lib as L
+    from dsa_attention import sparse_attention_from_mask, sparse_attention_hip
     from lightning_indexer import indexer_scores_hip
-    from topk_threshold import topk_threshold_into
+    from topk_threshold import topk_threshold_into, topk_threshold_mask
 
     B, T, k = cfg["B"], cfg["T"], cfg["k"]
     ins = gpu_inputs(cfg, dtype, dev, seed=3)
@@ -216,8 +217,17 @@ def bench_split_long(dev, cfg, dtype, name, reps, fp8_indexer=False):
     thr = torch.empty(B, T, 1, device=dev)
     out = torch.empty(B, T, cfg["HQ"], cfg["DV"], device=dev)
     ix = lambda: indexer_scores_hip(*ins[:3], write_upper=False, out=scores)  # noqa: E731
-    sel = lambda: topk_threshold_into(scores, min(k, T), thr, causal=True)  # noqa: E731
-    att = lambda: sparse_attention_hip(scores, thr, *ins[3:], out=out)  # noqa: E731
+    # The stages as dsa_split_hip runs them: where the attention runs on
+    # tiles from a bitmask, the select writes that bitmask in its own pass.
+    uses_mask = bool(L.lib().dsa_sparse_attn_uses_mask(L.dtype_code(dtype), T, cfg["HQ"],
+                                                       cfg["DQ"], cfg["DV"]))
+    if uses_mask:
+        mask = torch.empty(B, T, (T + 63) // 64, device=dev, dtype=torch.int64)
+        sel = lambda: topk_threshold_mask(scores, min(k, T), thr=thr, mask=mask)  # noqa: E731
+        att = lambda: sparse_attention_from_mask(mask, *ins[3:], out=out)  # noqa: E731
+    else:
+        sel = lambda: topk_threshold_into(scores, min(k, T), thr, causal=True)  # noqa: E731
+        att = lambda: sparse_attention_hip(scores, thr, *ins[3:], out=out)  # noqa: E731
 
     def fwd():
         ix()
@@ -238,7 +248,8 @@ def bench_split_long(dev, cfg, dtype, name, reps, fp8_indexer=False):
            "indexer_TFLOP_per_s": round(idx_fl / t_ix / 1e12, 1),
            "select_ms": round(t_sel * 1e3, 4),
            "select_GB_per_s": round((4.0 * B * T * (T + 1) / 2 + 4.0 * B * T) / t_sel / 1e9, 1),
-           "attention_ms": round(t_att * 1e3, 4)}
+           "attention_ms": round(t_att * 1e3, 4),
+           "select_writes_selection_bitmask": uses_mask}
     if fp8_indexer:
         # the same indexer on e4m3 q_idx/k_idx (w fp32): informational, the
         # split forward above runs the input dtype

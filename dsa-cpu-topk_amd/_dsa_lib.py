@@ -52,6 +52,7 @@ _SIGNATURES = {
     "dsa_fused_forward": ([_P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I, _I, _I, _I, _I, _I, _F,
                            _P, _P], _I),
     "dsa_selection_mask": ([_P, _I64, _P, _I64, _I64, _P, _I64, _P], _I),
+    "dsa_topk_threshold_mask": ([_P, _I64, _I64, _I64, _I, _P, _P, _I64, _P], _I),
     "dsa_sparse_attn_mask": ([_P, _I64, _P, _P, _P, _I, _I64, _I64, _I, _I, _I, _F, _P, _P], _I),
     "dsa_sparse_attn_uses_mask": ([_I, _I64, _I, _I, _I], _I),
     "dsa_sparse_attn_mask_noalloc": ([_P, _I64, _P, _P, _P, _P, _I, _I64, _I64, _I, _I, _I, _F,

@@ -156,6 +156,24 @@ int dsa_topk_threshold(const float* scores, int64_t rows, int64_t n, int64_t ld,
                     "dsa_topk_threshold");
 }
 
+int dsa_topk_threshold_mask(const float* scores, int64_t B, int64_t T, int64_t ld, int k,
+                            float* thr, uint64_t* mask, int64_t ldm, void* stream) {
+  if (B < 0 || T < 0) return fail(DSA_EINVAL, "topk_mask: negative size B=%lld T=%lld", (long long)B, (long long)T);
+  if (k <= 0) return fail(DSA_EINVAL, "topk_mask: k must be > 0 (got %d)", k);
+  if (k > T) return fail(DSA_EINVAL, "topk_mask: k must be <= T (k=%d, T=%lld)", k, (long long)T);
+  if (T > kMaxElems) return fail(DSA_EINVAL, "topk_mask: T=%lld >= 2^31", (long long)T);
+  if (ld < T) return fail(DSA_EINVAL, "topk_mask: ld=%lld < T=%lld", (long long)ld, (long long)T);
+  if (ldm < (T + 63) / 64)
+    return fail(DSA_EINVAL, "topk_mask: ldm=%lld < ceil(T/64)=%lld", (long long)ldm, (long long)((T + 63) / 64));
+  if (B * T == 0) return DSA_OK;
+  if (B * T > kMaxElems) return fail(DSA_EINVAL, "topk_mask: B*T=%lld rows >= 2^31", (long long)(B * T));
+  if (!scores || !thr || !mask) return fail(DSA_EINVAL, "topk_mask: null pointer");
+  if ((reinterpret_cast<uintptr_t>(mask) & 7u) != 0) return fail(DSA_EINVAL, "topk_mask: mask must be 8-byte aligned");
+  return hip_status(dsa::launch_topk_mask(scores, B, T, ld, k, thr, mask, ldm,
+                                          static_cast<hipStream_t>(stream)),
+                    "dsa_topk_threshold_mask");
+}
+
 int dsa_sparse_attn_threshold(const float* scores, int64_t ld, const float* thr, const void* Q,
                               const void* K, const void* V, int dtype, int64_t B, int64_t T,
                               int HQ, int DQ, int DV, float scale, float* out, void* stream) {

@@ -11,6 +11,11 @@ namespace dsa {
 // Radix-select: thr[r] = k-th largest of row r, optional exactly-k indices.
 hipError_t launch_topk(const float* scores, int64_t rows, int64_t n, int64_t ld, int k,
                        int64_t causal_T, float* thr, int32_t* idx, hipStream_t stream);
+// Causal thresholds of a [B,T,T] score matrix plus the rows' selection
+// bitmask (what launch_selection_mask writes), in one pass over the scores
+// where the bracket kernel serves the rows; otherwise the two launches.
+hipError_t launch_topk_mask(const float* scores, int64_t B, int64_t T, int64_t ld, int k,
+                            float* thr, uint64_t* mask, int64_t ldm, hipStream_t stream);
 
 // Lightning indexer.  dtype: 0 f32, 1 bf16, 2 f16, 3 fp8 e4m3 (w fp32).
 // ldq / ldk / ldw: elements from one token's q / k / w row to the next

@@ -59,6 +59,11 @@ struct SelectArgs {
   float* thr;
   int32_t* idx;
   int64_t nbatch;  // rows / causal_T in causal mode (set by the host)
+  // Causal rows only, threshold-only bracket kernel: also the row's
+  // selection bitmask (the words selection_mask_kernel writes), ldm words
+  // per row; null: none.
+  uint64_t* mask = nullptr;
+  int64_t ldm = 0;
 };
 
 // Row r of the 1-D causal order: q = r / nb (rows longest first), r % nb
@@ -108,6 +113,44 @@ __device__ __forceinline__ void row_of_block(const SelectArgs& a, int64_t& row,
 // Causal row with fewer than k real entries: the k-th largest of the full row
 // is one of the implicit -inf entries, and a stable sort puts the real
 // entries first, then the -inf ones in index order.
+// Selection bitmask of causal row `row` (query t, T = causal_T) for the
+// threshold th, once the block knows it: word w holds keys 64w .. 64w+63,
+// bit i set iff key 64w+i <= t and its score >= th (a NaN score or threshold
+// selects nothing); words 0 .. min(ceil(T/64)-1, (t|127)/64) are written,
+// those past the causal range as 0 -- what selection_mask_kernel writes
+// (tile_attn.hip), here from the row the block has just streamed, so the
+// re-read is served by the caches instead of HBM.  The block's waves split
+// the row's groups of 64 words; lane u of a wave keeps word 64c + u of its
+// group c, so each group is one coalesced 512-byte store.
+template <int NT>
+__device__ __forceinline__ void emit_mask_row(const SelectArgs& a, int64_t row, int t,
+                                              float th) {
+  constexpr int NW = NT / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  const int T = static_cast<int>(a.causal_T);
+  const float* __restrict__ srow = a.scores + row * a.ld;
+  uint64_t* __restrict__ mrow = a.mask + row * a.ldm;
+  const int W = (T + 63) / 64;
+  const int nw = min(W, ((t | 127) >> 6) + 1);
+  constexpr int U = 16;  // loads in flight per lane
+  for (int c = 64 * wid; c < nw; c += 64 * NW) {
+    const int nu = min(64, nw - c);
+    uint64_t mine = 0;
+    for (int u = 0; u < nu; u += U) {
+      float v[U];
+#pragma unroll
+      for (int e = 0; e < U; ++e) v[e] = srow[min(64 * (c + u + e) + lane, t)];  // in the row
+#pragma unroll
+      for (int e = 0; e < U; ++e) {
+        const uint64_t bits = ballot(64 * (c + u + e) + lane <= t && v[e] >= th);
+        mine = (lane == u + e) ? bits : mine;
+      }
+    }
+    if (lane < nu) mrow[c + lane] = mine;
+  }
+}
+
 template <int NT>
 __device__ __forceinline__ void emit_short_row(const SelectArgs& a, int64_t row) {
   if (threadIdx.x == 0) a.thr[row] = -__builtin_huge_valf();
@@ -805,8 +848,10 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
   int64_t row, nvalid;
   row_of_block(a, row, nvalid);
   const int k = a.k;
+  // (mask: causal rows, so the query is t = nvalid - 1; a.mask is uniform)
   if (nvalid < k) {
     emit_short_row<NT>(a, row);
+    if (!IDX && a.mask != nullptr) emit_mask_row<NT>(a, row, static_cast<int>(nvalid) - 1, -__builtin_huge_valf());
     return;
   }
   const float* __restrict__ src = a.scores + row * a.ld;
@@ -1203,11 +1248,16 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
         }
       }
     }
+    if (!IDX && a.mask != nullptr) {
+      block_sync_lds();  // wave 0's threshold in rsh
+      emit_mask_row<NT>(a, row, nv - 1, rsh[0]);
+    }
     return;
   }
   uint32_t krem;
   const uint32_t tk = stream_select<NT, true>(src, nvalid, k, lds, wsum, info, krem);
   if (tid == 0) a.thr[row] = key_to_float(tk);
+  if (!IDX && a.mask != nullptr) emit_mask_row<NT>(a, row, nv - 1, key_to_float(tk));
   if constexpr (IDX) {
     const int64_t nchunks = (nvalid + 4 * NT - 1) / (4 * NT);
     emit_indices<NT>(a.idx + row * static_cast<int64_t>(k), nchunks, tk, krem, wsum,
@@ -1589,6 +1639,28 @@ hipError_t launch_topk(const float* scores, int64_t rows, int64_t n, int64_t ld,
   if (cap <= 16384) return launch_reg<512, 32, 12>(a, vec, stream);
   if (cap <= 32768) return launch_reg<1024, 32, 12>(a, vec, stream);
   return launch_stream(a, vec, stream);
+}
+
+hipError_t launch_topk_mask(const float* scores, int64_t B, int64_t T, int64_t ld, int k,
+                            float* thr, uint64_t* mask, int64_t ldm, hipStream_t stream) {
+  if (B == 0 || T == 0) return hipSuccess;
+  const int64_t rows = B * T;
+  const bool vec = (T % 4 == 0) && (ld % 4 == 0) &&
+                   ((reinterpret_cast<uintptr_t>(scores) & 15u) == 0);
+  if (vec && bracket_fits(T, k)) {
+    // The rows the bracket kernel would select anyway: it writes each row's
+    // bitmask words as soon as it has the threshold (config 4: the mask
+    // kernel's second 537 MB read of the scores goes).
+    SelectArgs a{scores, rows, T, ld, k, T, thr, nullptr, B};
+    a.mask = mask;
+    a.ldm = ldm;
+    hipLaunchKernelGGL((topk_bracket_kernel<256, false>), dim3(static_cast<unsigned>(rows)),
+                       dim3(256), 0, stream, a);
+    return hipGetLastError();
+  }
+  const hipError_t e = launch_topk(scores, rows, T, ld, k, T, thr, nullptr, stream);
+  if (e != hipSuccess) return e;
+  return launch_selection_mask(scores, ld, thr, B, T, mask, ldm, stream);
 }
 
 }  // namespace dsa

@@ -26,7 +26,7 @@ import torch
 
 import _dsa_lib as L
 from lightning_indexer import indexer_scores_hip, indexer_scores_torch
-from topk_threshold import topk_threshold
+from topk_threshold import topk_threshold, topk_threshold_mask
 
 
 # ---------------------------------------------------------------------------
@@ -137,10 +137,21 @@ def selection_mask(scores: torch.Tensor, threshold: torch.Tensor) -> torch.Tenso
     return mask
 
 
-def _sparse_attention_mask(scores, thr, Q, K, V, dt, out):
+def sparse_attention_from_mask(mask: torch.Tensor, Q, K, V,
+                               out: torch.Tensor | None = None) -> torch.Tensor:
+    """Sparse attention on the dense-masked tiles with the selection given as
+    a bitmask (selection_mask or topk_threshold_mask): 16-bit Q/K/V, DQ = DV
+    in {64, 128} (DSAUnsupported otherwise)."""
+    L.require_gpu(mask, Q, K, V)
     B, T, HQ, DQ = Q.shape
     DV = V.shape[-1]
-    mask = selection_mask(scores, thr)
+    assert K.shape == (B, T, HQ, DQ) and V.shape == (B, T, HQ, DV), "K/V shapes"
+    W = (T + 63) // 64
+    assert (mask.dtype == torch.int64 and mask.is_contiguous() and mask.dim() == 3
+            and mask.shape[:2] == (B, T) and mask.shape[-1] >= W), "mask: int64 [B, T, >= ceil(T/64)]"
+    dt, Q, K, V = _attn_inputs(Q, K, V)
+    if out is None:
+        out = torch.empty(B, T, HQ, DV, device=Q.device, dtype=torch.float32)
     rc = L.lib().dsa_sparse_attn_mask(
         mask.data_ptr(), mask.shape[-1], Q.data_ptr(), K.data_ptr(), V.data_ptr(), L.dtype_code(dt),
         B, T, HQ, DQ, DV, 1.0 / math.sqrt(DQ), out.data_ptr(), L.stream_ptr(Q.device))
@@ -148,12 +159,26 @@ def _sparse_attention_mask(scores, thr, Q, K, V, dt, out):
     return out
 
 
+def _sparse_attention_mask(scores, thr, Q, K, V, dt, out):
+    return sparse_attention_from_mask(selection_mask(scores, thr), Q, K, V, out=out)
+
+
 def dsa_split_hip(q_idx, k_idx, w_idx, Q, K, V, top_k: int) -> torch.Tensor:
     """Split forward for any T: indexer (causal half only) -> causal
-    radix-select of the min(top_k,T)-th largest -> sparse attention."""
-    T = Q.shape[1]
+    radix-select of the min(top_k,T)-th largest -> sparse attention.  Where
+    the attention runs on tiles from a selection bitmask, the select writes
+    that bitmask in its own pass over the scores (topk_threshold_mask): the
+    same output as the three steps apart, bit for bit."""
+    B, T, HQ, DQ = Q.shape
+    DV = V.shape[-1]
     scores = indexer_scores_hip(q_idx, k_idx, w_idx, write_upper=False)
-    thr = topk_threshold(scores, min(top_k, T), causal=True)
+    k = min(top_k, T)
+    L.require_gpu(Q, K, V)
+    dt = L.common_dtype(Q, K, V)
+    if L.lib().dsa_sparse_attn_uses_mask(L.dtype_code(dt), T, HQ, DQ, DV):
+        _, mask = topk_threshold_mask(scores, k)
+        return sparse_attention_from_mask(mask, Q, K, V)
+    thr = topk_threshold(scores, k, causal=True)
     return sparse_attention_hip(scores, thr, Q, K, V)
 
 

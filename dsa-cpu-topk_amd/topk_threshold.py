@@ -105,6 +105,39 @@ def topk_threshold_batch_merge(scores: torch.Tensor, k: int) -> torch.Tensor:
     return _select(scores, k, False, False)[0]
 
 
+def topk_threshold_mask(scores: torch.Tensor, k: int, thr: torch.Tensor | None = None,
+                        mask: torch.Tensor | None = None):
+    """Causal thresholds of [B, T, T] GPU scores plus the selection bitmask
+    of those thresholds -- (thr [B, T, 1] fp32, mask [B, T, ceil(T/64)]
+    int64), the same as topk_threshold(scores, k, causal=True) followed by
+    dsa_attention.selection_mask(scores, thr), bit for bit, with the mask
+    written by the select's own pass over the scores where it can.
+    thr / mask: preallocated outputs (optional)."""
+    if scores.dim() != 3 or scores.shape[-2] != scores.shape[-1]:
+        raise RuntimeError("topk_threshold_mask needs [B, T, T] scores")
+    _check(scores, k)
+    L.require_gpu(scores)
+    B, T, _ = scores.shape
+    W = (T + 63) // 64
+    if thr is None:
+        thr = torch.empty(B, T, 1, device=scores.device, dtype=torch.float32)
+    if mask is None:
+        mask = torch.empty(B, T, W, device=scores.device, dtype=torch.int64)
+    if (thr.dtype != torch.float32 or not thr.is_contiguous() or thr.numel() != B * T
+            or thr.device != scores.device):
+        raise RuntimeError("thr must be a contiguous fp32 tensor of one value per row")
+    if (mask.dtype != torch.int64 or not mask.is_contiguous() or mask.shape != (B, T, W)
+            or mask.device != scores.device):
+        raise RuntimeError("mask must be a contiguous int64 [B, T, ceil(T/64)] tensor")
+    if B * T:
+        rc = L.lib().dsa_topk_threshold_mask(scores.data_ptr(), B, T, T, int(k), thr.data_ptr(),
+                                             mask.data_ptr(), W, L.stream_ptr(scores.device))
+        if rc != L.DSA_OK:
+            msg = L.lib().dsa_last_error().decode(errors="replace")
+            raise RuntimeError(f"topk_threshold_mask: {msg}")
+    return thr, mask
+
+
 def topk_indices(scores: torch.Tensor, k: int, causal: bool = False):
     """(threshold [...,1] fp32, indices [...,k] int32).
 

@@ -218,6 +218,23 @@ int dsa_selection_mask(const float* scores, int64_t ld, const float* thr, int64_
                        int64_t T, uint64_t* mask, int64_t ldm, void* stream);
 
 /*
+ * dsa_topk_threshold (causal, causal_T = T, rows = B*T, n = T) and
+ * dsa_selection_mask of its thresholds in one call: the same thr and mask,
+ * bit for bit.  Where the select's single-pass kernel serves the rows (rows
+ * above 4096 entries), that kernel writes each row's bitmask words as soon as
+ * it has the row's threshold, re-reading the row it has just streamed from
+ * the caches instead of HBM; other shapes run the two launches.  This is the
+ * split forward's select step when its attention runs on tiles.
+ * Replaces: scores.topk(...)[..., -1:] at dsa_attention.py:343-344 followed
+ *           by the `scores >= thr` selection of _sparse_attn_kernel
+ *           (dsa_attention.py:265-290); no reference counterpart as one call.
+ * Constraints: 1 <= k <= T < 2^31; B*T < 2^31; ld >= T;
+ *   ldm >= ceil(T/64); mask 8-byte aligned.
+ */
+int dsa_topk_threshold_mask(const float* scores, int64_t B, int64_t T, int64_t ld, int k,
+                            float* thr, uint64_t* mask, int64_t ldm, void* stream);
+
+/*
  * Sparse attention with the selection read from a dsa_selection_mask
  * bitmask: the dense-masked MFMA tile kernel, which reads 1 bit per
  * (query, key) instead of a 4-byte score (per head).  Together with

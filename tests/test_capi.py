@@ -214,6 +214,31 @@ def test_tiled_rejects_rows_past_4gib():
              None) == L.DSA_OK
 
 
+def test_topk_threshold_mask_checks():
+    """The select-plus-bitmask entry checks k, the row and mask widths, the
+    row count, null pointers and the mask's alignment before any HIP call;
+    B = 0 launches nothing."""
+    tm = L.lib().dsa_topk_threshold_mask
+    ok = [FAKE, 2, 300, 300, 10, FAKE, FAKE, 5, None]
+
+    def rc(**kw):
+        a = list(ok)
+        for k, v in kw.items():
+            a[int(k[1:])] = v
+        return _rc(tm, *a)[0]
+
+    assert rc(a4=0) == L.DSA_EINVAL               # k = 0
+    assert rc(a4=301) == L.DSA_EINVAL             # k > T
+    assert rc(a3=299) == L.DSA_EINVAL             # ld < T
+    assert rc(a7=4) == L.DSA_EINVAL               # ldm < ceil(T/64)
+    assert rc(a1=-1) == L.DSA_EINVAL              # negative B
+    assert rc(a1=1 << 30, a2=4, a3=4, a4=1, a7=1) == L.DSA_EINVAL  # B*T >= 2^31
+    assert rc(a0=None) == L.DSA_EINVAL            # null scores
+    assert rc(a6=None) == L.DSA_EINVAL            # null mask
+    assert rc(a6=FAKE + 4) == L.DSA_EINVAL        # misaligned mask
+    assert tm(FAKE, 0, 300, 300, 10, FAKE, FAKE, 5, None) == L.DSA_OK
+
+
 def test_selection_mask_and_mask_attention_checks():
     """Bitmask entry points: row width, dtype/shape coverage and the 32-bit
     mask-row offsets are checked before any HIP call; B = 0 launches

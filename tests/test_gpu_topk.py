@@ -10,7 +10,8 @@ import torch
 
 from helpers import say
 from oracle import dsa_oracle as O
-from topk_threshold import topk_indices, topk_threshold, topk_threshold_batch_merge
+from topk_threshold import (topk_indices, topk_threshold, topk_threshold_batch_merge,
+                            topk_threshold_mask)
 
 pytestmark = pytest.mark.gpu
 
@@ -178,6 +179,60 @@ def test_bracket_path_misses_fall_back(dev):
         say(f"topk bracket misses k={k}")
         torch.testing.assert_close(topk_threshold(xg, k).cpu(), O.topk_threshold(x, k),
                                    rtol=0, atol=0, equal_nan=True, msg=f"k={k}")
+
+
+def mask_words_cpu(srow, t, thr, T):
+    """Bitmask words of causal row t by the selection rule itself: bit i of
+    word w set iff key 64w + i <= t and srow[key] >= thr; words 0 ..
+    min(ceil(T/64) - 1, (t | 127) // 64)."""
+    W = (T + 63) // 64
+    nw = min(W, ((t | 127) >> 6) + 1)
+    keys = np.arange(64 * nw)
+    vals = np.full(64 * nw, np.nan, dtype=np.float32)
+    vals[: min(64 * nw, T)] = srow[: min(64 * nw, T)]
+    with np.errstate(invalid="ignore"):
+        sel = (keys <= t) & (vals >= thr)
+    bits = sel.reshape(nw, 64).astype(np.uint64) << np.arange(64, dtype=np.uint64)
+    return np.bitwise_or.reduce(bits, axis=1).view(np.int64)
+
+
+@pytest.mark.parametrize("B,T,k", [(1, 8192, 1), (1, 8192, 1000), (2, 4608, 300), (2, 2048, 64),
+                                   (1, 8192, 8192)])
+def test_threshold_mask_matches_two_launches(dev, B, T, k):
+    """topk_threshold_mask -- rows above 4096 entries: the single-pass select
+    writes each row's bitmask words once it has the row's threshold; shorter
+    rows: the select and the mask kernel -- equals topk_threshold(causal)
+    followed by selection_mask, bit for bit, on causal rows with NaN, +-inf,
+    heavy ties, a large chunk the select's sample skips and short rows
+    (t < k); entries above the diagonal hold 1e30, so a read past t shows.
+    Sampled rows are also checked against the selection rule on the CPU."""
+    from dsa_attention import selection_mask
+
+    g = torch.Generator().manual_seed(T + k)
+    s = torch.randn((B, T, T), generator=g)
+    s[0, :, ::97] = float("nan")
+    s[0, 3::5, 11::13] = float("inf")
+    s[-1, 1::3, 7::17] = float("-inf")
+    s[-1, ::4] = torch.randint(0, 3, (T,), generator=g).float()   # heavy ties
+    s[0, T - 1, 1024:2048] += 100.0                                # outside the sample
+    s[:, torch.ones(T, T, dtype=torch.bool).triu(1)] = 1e30
+    sg = s.to(dev)
+    say(f"topk+mask B={B} T={T} k={k}")
+    thr2, mask2 = topk_threshold_mask(sg, k)
+    thr1 = topk_threshold(sg, k, causal=True)
+    mask1 = selection_mask(sg, thr1)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(thr2.cpu(), thr1.cpu(), rtol=0, atol=0, equal_nan=True)
+    W = (T + 63) // 64
+    t = torch.arange(T)
+    written = torch.arange(W)[None, :] <= torch.clamp((t | 127) // 64, max=W - 1)[:, None]
+    m1, m2 = mask1.cpu(), mask2.cpu()
+    assert torch.equal(m2[:, written], m1[:, written])
+    thr_np, s_np, m2_np = thr2.cpu().numpy(), s.numpy(), m2.numpy()
+    for b in range(B):
+        for r in sorted({0, min(k, T) - 1, min(k, T - 1), T // 2, T - 1}):
+            want = mask_words_cpu(s_np[b, r], r, thr_np[b, r, 0], T)
+            assert np.array_equal(m2_np[b, r, : want.size], want), (b, r)
 
 
 @pytest.mark.parametrize("k", [1, 100, 2048, 3000, 16383])
