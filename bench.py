@@ -648,7 +648,7 @@ def pmc_workload(args, dev):
 
     import dsa_attention as D
     from lightning_indexer import indexer_scores_hip
-    from topk_threshold import topk_indices, topk_threshold
+    from topk_threshold import topk_indices, topk_threshold, topk_threshold_mask
 
     x = torch.ones(64 * 1024 * 1024, device=dev)
     y = torch.empty_like(x)
@@ -668,6 +668,8 @@ def pmc_workload(args, dev):
         thr = topk_threshold(scores, C4["k"], causal=True)
     for _ in range(2):                                      # thresholds + exactly-k indices
         topk_indices(scores, C4["k"], causal=True)
+    for _ in range(2):                                      # thresholds + the selection bitmask
+        topk_threshold_mask(scores, C4["k"])
     Q, K, V = gpu_inputs(C4, torch.bfloat16, dev, seed=5)[3:]
     out = torch.empty(1, C4["T"], C4["HQ"], C4["DV"], device=dev)
     for _ in range(2):   # selection bitmask + the tile kernel reading it, at this T

@@ -118,8 +118,9 @@ __device__ __forceinline__ void row_of_block(const SelectArgs& a, int64_t& row,
 // bit i set iff key 64w+i <= t and its score >= th (a NaN score or threshold
 // selects nothing); words 0 .. min(ceil(T/64)-1, (t|127)/64) are written,
 // those past the causal range as 0 -- what selection_mask_kernel writes
-// (tile_attn.hip), here from the row the block has just streamed, so the
-// re-read is served by the caches instead of HBM.  The block's waves split
+// (tile_attn.hip), here from the row the block has just streamed: the
+// re-read misses L2 but comes mostly from the MALL (config 4: 537 MB in
+// ~60 us, above HBM's peak rate), not HBM.  The block's waves split
 // the row's groups of 64 words; lane u of a wave keeps word 64c + u of its
 // group c, so each group is one coalesced 512-byte store.
 template <int NT>
