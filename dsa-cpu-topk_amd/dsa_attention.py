@@ -107,7 +107,7 @@ def sparse_attention_hip(scores: torch.Tensor, threshold: torch.Tensor, Q, K, V,
     if kernel is None and L.lib().dsa_sparse_attn_uses_mask(L.dtype_code(dt), T, HQ, DQ, DV):
         kernel = "mask"
     if kernel == "mask":
-        return _sparse_attention_mask(scores, thr, Q, K, V, dt, out)
+        return _sparse_attention_mask(scores, thr, Q, K, V, out)
     fn = {None: L.lib().dsa_sparse_attn_threshold,
           "tiled": L.lib().dsa_sparse_attn_threshold_tiled,
           "staged": L.lib().dsa_sparse_attn_threshold_staged}[kernel]
@@ -159,7 +159,7 @@ def sparse_attention_from_mask(mask: torch.Tensor, Q, K, V,
     return out
 
 
-def _sparse_attention_mask(scores, thr, Q, K, V, dt, out):
+def _sparse_attention_mask(scores, thr, Q, K, V, out):
     return sparse_attention_from_mask(selection_mask(scores, thr), Q, K, V, out=out)
 
 
