@@ -821,8 +821,12 @@ constexpr int kFinGather = 64;   // kept values of one finishing bin ranked in r
 // 64-position ranges places every selected entry at #(above before it) +
 // min(#(equal before it), k - #above), ascending positions -- emit_indices'
 // rule without a pass per chunk.
-template <int NT, bool IDX>
+template <int NT, bool IDX, bool MASK = false>
 __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
+  // IDX: exactly-k indices; MASK: the selection bitmask (a.mask), both from
+  // the row's flag bitmap below.
+  static_assert(!(IDX && MASK), "one output mode");
+  constexpr bool FLAGS = IDX || MASK;
   constexpr int NW = NT / kWave;
   constexpr int CH = 4 * NT;  // entries per chunk (one float4 per thread)
   constexpr int CAP = 19;     // LDS column slots per thread
@@ -832,7 +836,7 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
   // k indices of up to kIdxStage are staged in the columns' LDS afterwards.
   constexpr int kIdxMapWord = (kCandCap + kFinBins + kFinGather + 3) & ~3;
   constexpr int kIdxStage = CAP * NT;
-  static_assert(!IDX || kIdxMapWord + 16 * NT / 4 <= CAP * NT, "the IDX bitmap fits the columns");
+  static_assert(!FLAGS || kIdxMapWord + 16 * NT / 4 <= CAP * NT, "the flag bitmap fits the columns");
   // lds: sample histogram [0, kBrBins), then per-thread columns (slot s of
   // thread t at s*NT + t), then the compacted kept list [0, n_kept) with the
   // finishing wave's histogram and gather list at kCandCap.
@@ -957,21 +961,24 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
   uint32_t below = 0, kc = 0;  // this thread: valid values below fhi; kept
   bool bad = false;            // wave-uniform: a column came near CAP
   uint32_t* col = lds + tid;
-  uint64_t abv = 0, kpt = 0;   // IDX: entries above the interval; kept entries
-  // Returns bit 0: kept, bit 1: above the interval (NaN included).
+  uint64_t abv = 0, kpt = 0;   // FLAGS: entries above the interval; kept entries
+  // Returns bit 0: kept, bit 1: above the interval (NaN included), bit 2: NaN.
   auto take = [&](float v, bool valid) -> uint32_t {
     const bool lt = valid && v < fhi;
     const bool kp = lt && !(v < flo);
     col[kc * NT] = __float_as_uint(v);  // the next free slot; kept only if kc advances
     below += lt ? 1u : 0u;
     kc += kp ? 1u : 0u;
-    return (kp ? 1u : 0u) | ((valid && !lt) ? 2u : 0u);
+    return (kp ? 1u : 0u) | ((valid && !lt) ? 2u : 0u) | ((valid && v != v) ? 4u : 0u);
   };
-  // IDX: a chunk's 4 results into the masks (chunk j, streaming slot sl).
+  // FLAGS: a chunk's 4 results into the masks (chunk j, streaming slot sl).
+  // Indices rank NaN first (torch.topk's order); the bitmask selects by
+  // score >= thr, which no NaN passes, so MASK leaves NaN out of "above".
   auto record = [&](uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3, int j, int sl) {
-    if constexpr (IDX) {
+    if constexpr (FLAGS) {
+      auto ab = [](uint32_t r) { return MASK ? ((r >> 1) & ~(r >> 2) & 1u) : ((r >> 1) & 1u); };
       const uint32_t nk = (r0 & 1u) | ((r1 & 1u) << 1) | ((r2 & 1u) << 2) | ((r3 & 1u) << 3);
-      const uint32_t na = (r0 >> 1) | ((r1 >> 1) << 1) | ((r2 >> 1) << 2) | ((r3 >> 1) << 3);
+      const uint32_t na = ab(r0) | (ab(r1) << 1) | (ab(r2) << 2) | (ab(r3) << 3);
       abv |= static_cast<uint64_t>(na) << (4 * j);
       kpt |= static_cast<uint64_t>(nk) << (4 * sl);
     } else {
@@ -1072,12 +1079,12 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
 #pragma unroll
     for (int s = 0; s < CAP; ++s)
       if (static_cast<uint32_t>(s) < kc) lds[kbase + s] = mine[s];
-    // IDX: the row's flags as an LDS bitmap in position order, past what the
-    // finishing wave uses: byte j*NT+t holds positions (j*NT+t)*4 .. +3,
+    // FLAGS: the row's flags as an LDS bitmap in position order, past what
+    // the finishing wave uses: byte j*NT+t holds positions (j*NT+t)*4 .. +3,
     // above the threshold in the low nibble, equal to it in the high one.
     // The values above the interval go in now, while wave 0 finishes.
     uint8_t* fb = reinterpret_cast<uint8_t*>(lds + kIdxMapWord);
-    if constexpr (IDX) {
+    if constexpr (FLAGS) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) fb[j * NT + tid] = static_cast<uint8_t>((abv >> (4 * j)) & 15u);
     }
@@ -1165,7 +1172,7 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
         rsh[0] = res + 0.0f;
       }
     }  // wave 0
-    if constexpr (IDX) {
+    if constexpr (FLAGS) {
       block_sync_lds();
       const float thr = rsh[0];
       // This thread's kept values (its kc entries of the kept list, in its
@@ -1194,62 +1201,70 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
                (static_cast<uint64_t>(w16(v.z)) << 32) | (static_cast<uint64_t>(w16(v.w)) << 48);
       };
       const uint64_t G = nib(fv, 0), Eq = nib(fv, 4);
-      uint32_t tot;
-      const uint32_t ex = block_exclusive_sum<NT>(
-          static_cast<uint32_t>(__builtin_popcountll(G)) |
-              (static_cast<uint32_t>(__builtin_popcountll(Eq)) << 16),
-          wsum, tot);  // its barriers also order the bitmap reads before the staging
-      const uint32_t kq = ku - (tot & 0xffffu);  // equal values taken, lowest positions first
-      int32_t* out = a.idx + row * static_cast<int64_t>(k);
-      const bool staged = k <= kIdxStage;
-      int32_t* so = reinterpret_cast<int32_t*>(lds);
-      uint32_t gb = ex & 0xffffu, eb = ex >> 16;
-      if ((tot >> 16) <= kq) {
-        // Every equal value is taken (the usual case): an entry's slot is its
-        // rank among the selected ones.
-        uint32_t slot = gb + eb;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          for (uint32_t m = static_cast<uint32_t>((G | Eq) >> (32 * h)); m != 0u; m &= m - 1u) {
-            const int32_t pos = 64 * tid + 32 * h + static_cast<int32_t>(__builtin_ctz(m));
-            if (staged) so[slot] = pos;
-            else out[slot] = pos;
-            ++slot;
-          }
-        }
+      if constexpr (MASK) {
+        // Word tid of the row's selection bitmask: positions 64 tid .. +63
+        // at or above thr.  Positions past the row hold no flags, so the
+        // words up to the end of the row's 128-query block are 0 there.
+        const int nw = min(static_cast<int>((a.causal_T + 63) / 64), (((nv - 1) | 127) >> 6) + 1);
+        if (tid < nw) a.mask[row * a.ldm + tid] = G | Eq;
       } else {
-        for (uint64_t m = G | Eq; m != 0u; m &= m - 1u) {
-          const int bp = static_cast<int>(__builtin_ctzll(m));
-          const int32_t pos = 64 * tid + bp;
-          int32_t slot = -1;
-          if ((G >> bp) & 1u) {
-            slot = static_cast<int32_t>(gb + (eb < kq ? eb : kq));
-            ++gb;
-          } else {
-            if (eb < kq) slot = static_cast<int32_t>(gb + eb);
-            ++eb;
+        uint32_t tot;
+        const uint32_t ex = block_exclusive_sum<NT>(
+            static_cast<uint32_t>(__builtin_popcountll(G)) |
+                (static_cast<uint32_t>(__builtin_popcountll(Eq)) << 16),
+            wsum, tot);  // its barriers also order the bitmap reads before the staging
+        const uint32_t kq = ku - (tot & 0xffffu);  // equal values taken, lowest positions first
+        int32_t* out = a.idx + row * static_cast<int64_t>(k);
+        const bool staged = k <= kIdxStage;
+        int32_t* so = reinterpret_cast<int32_t*>(lds);
+        uint32_t gb = ex & 0xffffu, eb = ex >> 16;
+        if ((tot >> 16) <= kq) {
+          // Every equal value is taken (the usual case): an entry's slot is its
+          // rank among the selected ones.
+          uint32_t slot = gb + eb;
+  #pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            for (uint32_t m = static_cast<uint32_t>((G | Eq) >> (32 * h)); m != 0u; m &= m - 1u) {
+              const int32_t pos = 64 * tid + 32 * h + static_cast<int32_t>(__builtin_ctz(m));
+              if (staged) so[slot] = pos;
+              else out[slot] = pos;
+              ++slot;
+            }
           }
-          if (slot >= 0) {
-            if (staged) so[slot] = pos;
-            else out[slot] = pos;
+        } else {
+          for (uint64_t m = G | Eq; m != 0u; m &= m - 1u) {
+            const int bp = static_cast<int>(__builtin_ctzll(m));
+            const int32_t pos = 64 * tid + bp;
+            int32_t slot = -1;
+            if ((G >> bp) & 1u) {
+              slot = static_cast<int32_t>(gb + (eb < kq ? eb : kq));
+              ++gb;
+            } else {
+              if (eb < kq) slot = static_cast<int32_t>(gb + eb);
+              ++eb;
+            }
+            if (slot >= 0) {
+              if (staged) so[slot] = pos;
+              else out[slot] = pos;
+            }
           }
         }
-      }
-      if (staged) {
-        block_sync_lds();
-        // 16-byte stores when the row allows them; streamed past the caches
-        // (the index rows are not re-read by this kernel)
-        typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-        if ((k & 3) == 0 && (reinterpret_cast<uintptr_t>(a.idx) & 15u) == 0u) {
-          const i32x4* s4 = reinterpret_cast<const i32x4*>(so);
-          i32x4* o4 = reinterpret_cast<i32x4*>(out);
-          for (int i = tid; i < k / 4; i += NT) __builtin_nontemporal_store(s4[i], o4 + i);
-        } else {
-          for (int i = tid; i < k; i += NT) out[i] = so[i];
+        if (staged) {
+          block_sync_lds();
+          // 16-byte stores when the row allows them; streamed past the caches
+          // (the index rows are not re-read by this kernel)
+          typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+          if ((k & 3) == 0 && (reinterpret_cast<uintptr_t>(a.idx) & 15u) == 0u) {
+            const i32x4* s4 = reinterpret_cast<const i32x4*>(so);
+            i32x4* o4 = reinterpret_cast<i32x4*>(out);
+            for (int i = tid; i < k / 4; i += NT) __builtin_nontemporal_store(s4[i], o4 + i);
+          } else {
+            for (int i = tid; i < k; i += NT) out[i] = so[i];
+          }
         }
       }
     }
-    if (!IDX && a.mask != nullptr) {
+    if (!FLAGS && a.mask != nullptr) {
       block_sync_lds();  // wave 0's threshold in rsh
       emit_mask_row<NT>(a, row, nv - 1, rsh[0]);
     }
@@ -1651,12 +1666,18 @@ hipError_t launch_topk_mask(const float* scores, int64_t B, int64_t T, int64_t l
   if (vec && bracket_fits(T, k)) {
     // The rows the bracket kernel would select anyway: it writes each row's
     // bitmask words as soon as it has the threshold (config 4: the mask
-    // kernel's second 537 MB read of the scores goes).
+    // kernel's second 537 MB read of the scores goes).  Rows of up to 16
+    // chunks take the words from the flag bitmap the index output uses (no
+    // second read of the row at all); longer rows re-read it.
     SelectArgs a{scores, rows, T, ld, k, T, thr, nullptr, B};
     a.mask = mask;
     a.ldm = ldm;
-    hipLaunchKernelGGL((topk_bracket_kernel<256, false>), dim3(static_cast<unsigned>(rows)),
-                       dim3(256), 0, stream, a);
+    if (T <= kBracketIdxMaxN)
+      hipLaunchKernelGGL((topk_bracket_kernel<256, false, true>), dim3(static_cast<unsigned>(rows)),
+                         dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((topk_bracket_kernel<256, false>), dim3(static_cast<unsigned>(rows)),
+                         dim3(256), 0, stream, a);
     return hipGetLastError();
   }
   const hipError_t e = launch_topk(scores, rows, T, ld, k, T, thr, nullptr, stream);

@@ -222,9 +222,9 @@ int dsa_selection_mask(const float* scores, int64_t ld, const float* thr, int64_
  * dsa_selection_mask of its thresholds in one call: the same thr and mask,
  * bit for bit.  Where the select's single-pass kernel serves the rows (rows
  * above 4096 entries), that kernel writes each row's bitmask words as soon as
- * it has the row's threshold, re-reading the row it has just streamed (on
- * MI355X mostly from the MALL rather than HBM); other shapes run the two
- * launches.  This is the
+ * it has the row's threshold: from the flag bitmap it keeps of the row (rows
+ * up to 16384 entries), else by re-reading the row it has just streamed;
+ * other shapes run the two launches.  This is the
  * split forward's select step when its attention runs on tiles.
  * Replaces: scores.topk(...)[..., -1:] at dsa_attention.py:343-344 followed
  *           by the `scores >= thr` selection of _sparse_attn_kernel

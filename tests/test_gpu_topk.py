@@ -197,10 +197,12 @@ def mask_words_cpu(srow, t, thr, T):
 
 
 @pytest.mark.parametrize("B,T,k", [(1, 8192, 1), (1, 8192, 1000), (2, 4608, 300), (2, 2048, 64),
-                                   (1, 8192, 8192)])
+                                   (1, 8192, 8192), (1, 16448, 1000)])
 def test_threshold_mask_matches_two_launches(dev, B, T, k):
-    """topk_threshold_mask -- rows above 4096 entries: the single-pass select
-    writes each row's bitmask words once it has the row's threshold; shorter
+    """topk_threshold_mask -- rows of 4097-16384 entries: the single-pass
+    select writes each row's bitmask words from its own flag bitmap once it
+    has the row's threshold (NaN, which indices rank first, selects nothing
+    here); longer rows (T = 16448): it re-reads the row for them; shorter
     rows: the select and the mask kernel -- equals topk_threshold(causal)
     followed by selection_mask, bit for bit, on causal rows with NaN, +-inf,
     heavy ties, a large chunk the select's sample skips and short rows
