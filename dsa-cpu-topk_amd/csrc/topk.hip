@@ -900,12 +900,19 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
   // become NaN here).  An infinite end is replaced by the finite range.
   auto block_range = [&](bool finite_only, float& vmin, float& vmax) {
     float hi = -__builtin_huge_valf(), lo = __builtin_huge_valf();
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float v = (!whole || sample_in(i)) ? sv[i] : __builtin_nanf("");
+    // (two copies on the block-uniform `whole`: only rows that are their
+    // own sample test each entry against the row's end)
+    auto extend = [&](float v) {
       if (finite_only) v = fabsf(v) <= __FLT_MAX__ ? v : __builtin_nanf("");
       hi = fmaxf(hi, v);
       lo = fminf(lo, v);
+    };
+    if (whole) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) extend(sample_in(i) ? sv[i] : __builtin_nanf(""));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) extend(sv[i]);
     }
     hi = wave_extreme_f32<true>(hi);
     lo = wave_extreme_f32<false>(lo);
@@ -938,10 +945,13 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
     scale = 0.0f;
     vmin = 0.0f;
   }
+  if (whole) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    if (!whole || sample_in(i))
-      atomicAdd(&lds[value_bin(sv[i], vmin, scale, kBrBins - 1)], 1u);
+    for (int i = 0; i < 16; ++i)
+      if (sample_in(i)) atomicAdd(&lds[value_bin(sv[i], vmin, scale, kBrBins - 1)], 1u);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) atomicAdd(&lds[value_bin(sv[i], vmin, scale, kBrBins - 1)], 1u);
   }
   block_sync_lds();
   {
