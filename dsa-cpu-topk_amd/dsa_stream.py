@@ -36,6 +36,17 @@ from lightning_indexer import indexer_scores_hip
 from topk_threshold import topk_threshold_into
 
 
+def _refuse_capture(what: str) -> None:
+    """The two-stream pipeline is eager only.  Capturing it into one graph
+    crashed the host process inside the runtime's end of capture (cause not
+    established), so a call made while the current stream is capturing is
+    refused before it enqueues anything; DSAStreamGraph is the captured form
+    (one stream)."""
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(f"DSAStreamPipeline.{what}: the two-stream pipeline cannot be "
+                           "captured into a graph; use DSAStreamGraph (one stream)")
+
+
 class DSAStreamPipeline:
     """Streams batches of one shape [B,T,...] through the split forward.
 
@@ -43,6 +54,8 @@ class DSAStreamPipeline:
     output tensor [B,T,HQ,DV] fp32, valid once `synchronize()` (or an event
     recorded on `attention_stream` after it) has completed.  Inputs must
     stay alive and unchanged until then; the pipeline keeps a reference.
+    submit() and join() raise RuntimeError while the current stream is
+    being captured: the pipeline is not capturable.
     """
 
     def __init__(self, B: int, T: int, top_k: int, device="cuda", depth: int = 2):
@@ -60,6 +73,7 @@ class DSAStreamPipeline:
         self._n = 0
 
     def submit(self, q_idx, k_idx, w_idx, Q, K, V) -> torch.Tensor:
+        _refuse_capture("submit")
         L.require_gpu(q_idx, k_idx, w_idx, Q, K, V)
         B, T = Q.shape[0], Q.shape[1]
         assert (B, T) == (self.B, self.T), f"batch shape {(B, T)} != pipeline {(self.B, self.T)}"
@@ -88,7 +102,8 @@ class DSAStreamPipeline:
 
     def join(self) -> None:
         """Order the caller's stream after every submitted batch (no host
-        wait; also valid while the caller's stream is being captured)."""
+        wait).  Not valid under graph capture (see `_refuse_capture`)."""
+        _refuse_capture("join")
         caller = torch.cuda.current_stream(self.device)
         caller.wait_stream(self.attention_stream)
         caller.wait_stream(self.indexer_stream)
@@ -102,7 +117,7 @@ class DSAStreamPipeline:
 
     def reset(self) -> None:
         """Forget slot-reuse events of earlier submissions (after a
-        synchronize, before a graph capture)."""
+        synchronize)."""
         self._done = [None] * self.depth
         self._keep.clear()
         self._n = 0

@@ -266,6 +266,10 @@ int dsa_sparse_attn_mask(const uint64_t* mask, int64_t ldm, const void* Q, const
  *   DSA_EINVAL.  Shapes: those of dsa_sparse_attn_mask (bf16/fp16,
  *   DQ = DV in {64, 128}); ld >= T.  Calls that overlap in time on one GPU
  *   share the array and race; the device is the current one.
+ * Graph capture: a device's first call looks up the array's address
+ *   (hipGetSymbolAddress), so make that first call eagerly, outside any
+ *   capture; later calls enqueue kernels only (no memset, no allocation)
+ *   and may be captured.
  */
 int dsa_sparse_attn_mask_noalloc(const float* scores, int64_t ld, const float* thr,
                                  const void* Q, const void* K, const void* V, int dtype,

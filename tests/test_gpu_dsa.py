@@ -163,6 +163,27 @@ def test_config4(dev):
                  rtol=2e-2, atol=2e-2)
 
 
+def test_config4_split_equals_threshold_tile_kernel(dev):
+    """The config-4 split forward runs the select writing the bitmask
+    (topk_threshold_mask) and the tile kernel on that bitmask; its full
+    output, all 16384 rows, equals bit for bit the tile kernel that reads
+    the scores and a threshold from the threshold-only select
+    (dsa_attention.py:343-345 as three steps)."""
+    from topk_threshold import topk_threshold
+
+    ins, k = inputs("c4")
+    g = to_dev(ins, dev)
+    del ins
+    say("config 4 split forward vs threshold tile kernel, all rows")
+    split = D.dsa_split_hip(*g, k)
+    s = indexer_scores_hip(*g[:3], write_upper=False)
+    thr = topk_threshold(s, k, causal=True)
+    tiled = D.sparse_attention_hip(s, thr, *g[3:], kernel="tiled")
+    torch.cuda.synchronize()
+    assert not bool(torch.isnan(split).any())
+    assert torch.equal(split, tiled)
+
+
 def test_hybrid_path_with_reference_cpu_threshold(dev):
     """dsa_hybrid.py:46-66: the hybrid drop-in equals the split forward, and a
     threshold made on the CPU by this repo's port of the reference's AVX-512

@@ -237,6 +237,50 @@ def test_threshold_mask_matches_two_launches(dev, B, T, k):
             assert np.array_equal(m2_np[b, r, : want.size], want), (b, r)
 
 
+@pytest.mark.parametrize("k", [1, 2048, 16384])
+def test_threshold_mask_config4_full(dev, k):
+    """The select form the config-4 split forward runs -- topk_threshold_mask
+    at B=1, T=16384 (the bracket kernel's MASK form, bitmap path) -- at full
+    size: thresholds and every written bitmask word equal
+    topk_threshold(causal) + selection_mask bit for bit on all 16384 rows,
+    with NaN columns, +-inf entries, heavy-tie rows, a chunk the sample
+    skips and 1e30 above the diagonal (a read past t shows); sampled rows
+    against the selection rule on the CPU.  k = 1 (NaN rows give a NaN
+    threshold), 2048 (config 4), 16384 (every row but the last is short)."""
+    from dsa_attention import selection_mask
+
+    T = 16384
+    g = torch.Generator(device=dev).manual_seed(1000 + k)
+    s = torch.randn((1, T, T), generator=g, device=dev)
+    s[0, :, ::97] = float("nan")
+    s[0, 3::5, 11::13] = float("inf")
+    s[0, 1::3, 7::17] = float("-inf")
+    s[0, ::4] = torch.randint(0, 3, (T,), generator=g, device=dev).float()   # heavy ties
+    s[0, T - 1, 1024:2048] += 100.0                                         # outside the sample
+    s[0].masked_fill_(torch.ones(T, T, dtype=torch.bool, device=dev).triu_(1), 1e30)
+    say(f"topk+mask config-4 full size k={k}")
+    thr2, mask2 = topk_threshold_mask(s, k)
+    thr1 = topk_threshold(s, k, causal=True)
+    mask1 = selection_mask(s, thr1)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(thr2, thr1, rtol=0, atol=0, equal_nan=True)
+    W = T // 64
+    t = torch.arange(T, device=dev)
+    written = torch.arange(W, device=dev)[None, :] <= torch.clamp((t | 127) // 64, max=W - 1)[:, None]
+    assert torch.equal(mask2[:, written], mask1[:, written])
+    del mask1
+    thr_np = thr2.cpu().numpy()
+    for r in sorted({0, 1, min(k, T) - 1, min(k, T - 1), 4096, T // 2, T - 2, T - 1}):
+        want = mask_words_cpu(s[0, r].cpu().numpy(), r, thr_np[0, r, 0], T)
+        assert np.array_equal(mask2[0, r, : want.size].cpu().numpy(), want), r
+    # thresholds of sampled rows against the oracle on the same entries
+    rows = [0, 2047, 2048, 9999, T - 1]
+    srows = s[0, rows].cpu()
+    causal = torch.arange(T)[None, :] <= torch.tensor(rows)[:, None]
+    want_thr = O.topk_threshold(srows.masked_fill(~causal, float("-inf")), k)
+    torch.testing.assert_close(thr2[0, rows].cpu(), want_thr, rtol=0, atol=0, equal_nan=True)
+
+
 @pytest.mark.parametrize("k", [1, 100, 2048, 3000, 16383])
 def test_bracket_indices_single_pass(dev, k):
     """Thresholds with exactly-k indices of rows up to 16384 entries come from

@@ -121,3 +121,21 @@ def test_fuse_projection_weights_matches_cache():
     wc = LI.fuse_projection_weights(*ws)
     assert wc.shape == (32, 36)
     _check(wc, ws)
+
+
+def test_stream_pipeline_refuses_capture(monkeypatch):
+    """DSAStreamPipeline is eager only: submit() and join() raise while the
+    current stream is capturing, before anything is enqueued.  The capture
+    state is faked from the host; no graph is captured."""
+    import pytest
+
+    import dsa_stream
+
+    pipe = dsa_stream.DSAStreamPipeline.__new__(dsa_stream.DSAStreamPipeline)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    with pytest.raises(RuntimeError, match="cannot be captured"):
+        pipe.submit(None, None, None, None, None, None)
+    with pytest.raises(RuntimeError, match="cannot be captured"):
+        pipe.join()
+    with pytest.raises(RuntimeError, match="cannot be captured"):
+        pipe.synchronize()
