@@ -384,25 +384,7 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
     for (int qt = 0; qt < 2; ++qt)
       mw[qt] = __builtin_bit_cast(uint64_t, buffer_load_f32x2(rs, static_cast<int>(soff[qt]), 0, 0));
   };
-  // Entry (qt, j, r) of lane group g is key 16j + 4g + r of the tile: bit
-  // 16j + r of the word shifted right by 4g.
-  auto make_sel_words = [&](const uint64_t (&mw)[2], bool (&sel)[2][4][4]) {
-    bool any = false;
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      const uint64_t w = mw[qt] >> (4 * g);
-      const uint32_t half[2] = {static_cast<uint32_t>(w), static_cast<uint32_t>(w >> 32)};
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          sel[qt][j][r] = (half[j >> 1] & (1u << (16 * (j & 1) + r))) != 0u;
-          any |= sel[qt][j][r];
-        }
-    }
-    return __ballot(any) != 0;
-  };
-
+  uint64_t mwc[2] = {0, 0};  // bitmask words of the tile compute() works on
   // Everything one wave does with key tile kt, staged in (kl, vl).
   auto compute = [&](const bool (&sel)[2][4][4], const DSA_LDS uint8_t* kl,
                      const DSA_LDS uint8_t* vl) __attribute__((always_inline)) {
@@ -447,7 +429,21 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          st[j][qt][r] = sel[qt][j][r] ? st[j][qt][r] : -__builtin_huge_valf();
+          if constexpr (MASK) {
+            // entry (j, r) of lane group g is bit 16j + r of the word shifted
+            // right by 4g: a sign-extended bit field (0 or ~0) and a bit
+            // select of the logit or -inf, two VALU instructions.  Scalars
+            // move between float and integer through __float_as_uint /
+            // __uint_as_float: this toolchain miscompiles __builtin_bit_cast
+            // of a vector element (every element then reads element 0).
+            const uint32_t hw = static_cast<uint32_t>((mwc[qt] >> (4 * g)) >> (32 * (j >> 1)));
+            const uint32_t keep =
+                static_cast<uint32_t>(static_cast<int32_t>(hw << (31 - (16 * (j & 1) + r))) >> 31);
+            const float x = st[j][qt][r];
+            st[j][qt][r] = __uint_as_float((__float_as_uint(x) & keep) | (0xff800000u & ~keep));
+          } else {
+            st[j][qt][r] = sel[qt][j][r] ? st[j][qt][r] : -__builtin_huge_valf();
+          }
       float mx = -__builtin_huge_valf();
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -536,7 +532,11 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
   auto step = [&](auto interior, int kt, DSA_LDS uint8_t* kc, DSA_LDS uint8_t* vc,
                   DSA_LDS uint8_t* kn, DSA_LDS uint8_t* vn) __attribute__((always_inline)) {
     bool act;
-    if constexpr (MASK) act = make_sel_words(mw, sel);
+    if constexpr (MASK) {  // the words are kept: the prefetch below overwrites mw
+      act = __ballot((mw[0] | mw[1]) != 0) != 0;
+      mwc[0] = mw[0];
+      mwc[1] = mw[1];
+    }
     else act = decltype(interior)::value ? make_sel_fast(sv, sel) : make_sel(kt, sv, sel);
     const bool more = kt + 1 < nkt;
     if (more) {
