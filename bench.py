@@ -348,6 +348,13 @@ def time_reference_style(fn, stream, warmup=5, iters=20):
     return a.elapsed_time(b) / iters
 
 
+# The reference's published end-to-end table (README.md:49-55): GPU fused
+# and CPU hybrid ms on its RTX PRO 6000 + Ryzen 9 9950X3D.
+REF_HYBRID = {(16, 512, 32): (5.62, 4.68), (16, 512, 64): (5.66, 5.47), (32, 512, 64): (11.98, 11.72),
+              (64, 512, 64): (25.96, 24.97), (16, 512, 128): (5.67, 8.39), (4, 512, 64): (1.34, 1.56),
+              (16, 128, 16): (0.10, 0.20)}
+
+
 def bench_hybrid(dev):
     """The reference's experiment (bench_hybrid.py:40-53, dsa_hybrid.py:46-66)
     on this box: the whole CPU-offload forward -- GPU indexer, pinned d2h, host
@@ -363,8 +370,10 @@ def bench_hybrid(dev):
 
     stream = torch.cuda.current_stream(dev)
     rows = []
-    for B, k in [(C1["B"], C1["k"])] + [(b, kk) for b, kk, _ in C2_SWEEP]:
-        cfg = dict(C1, B=B, k=k)
+    # config 1, the config-2 sweep, and the reference's T=128 row (README.md:55)
+    for B, T, k in ([(C1["B"], C1["T"], C1["k"])] + [(b, C1["T"], kk) for b, kk, _ in C2_SWEEP]
+                    + [(16, 128, 16)]):
+        cfg = dict(C1, B=B, T=T, k=k)
         ins = gpu_inputs(cfg, torch.float32, dev, seed=B + k)
         ctx = HybridContext(B, cfg["T"], device=dev)
         hyb = dsa_hybrid_cpu_topk(*ins, k, ctx=ctx)
@@ -377,6 +386,8 @@ def bench_hybrid(dev):
                                                                causal=True),
         }
         row = {"B": B, "T": cfg["T"], "k": k, "hybrid_equals_split": equal}
+        if (B, T, k) in REF_HYBRID:
+            row["reference_fused_ms"], row["reference_hybrid_ms"] = REF_HYBRID[(B, T, k)]
         for name, fn in legs.items():
             row[name] = round(time_reference_style(fn, stream), 4)
         rows.append(row)
@@ -457,7 +468,7 @@ def bench_select_c4(dev, reps=20):
     import torch
 
     from lightning_indexer import indexer_scores_hip
-    from topk_threshold import topk_indices, topk_threshold
+    from topk_threshold import topk_indices, topk_threshold, topk_threshold_mask
 
     T, k = C4["T"], C4["k"]
     ins = gpu_inputs(C4, torch.bfloat16, dev, seed=4)
@@ -468,9 +479,17 @@ def bench_select_c4(dev, reps=20):
     t_thr = time_events(lambda: topk_threshold(scores, k, causal=True), reps, stream)
     warm(lambda: topk_indices(scores, k, causal=True))
     t_idx = time_events(lambda: topk_indices(scores, k, causal=True), reps, stream)
+    thr_buf = torch.empty(1, T, 1, device=dev)
+    W = (T + 63) // 64
+    mask = torch.empty(1, T, W, device=dev, dtype=torch.int64)
+    sel_mask = lambda: topk_threshold_mask(scores, k, thr=thr_buf, mask=mask)  # noqa: E731
+    warm(sel_mask)
+    t_mask = time_events(sel_mask, reps, stream)
     read = 4.0 * T * (T + 1) / 2
     out_thr = 4.0 * T
     out_idx = out_thr + 4.0 * T * k
+    # bitmask words written: row t writes words 0 .. min(W, (t|127)/64 + 1) - 1
+    out_mask = out_thr + 8.0 * sum(min(W, ((t | 127) >> 6) + 1) for t in range(T))
     res = {
         "workload": "causal radix-select, config-4 indexer scores [1,16384,16384] fp32, k=2048",
         "ms": round(t_thr * 1e3, 4),
@@ -479,6 +498,13 @@ def bench_select_c4(dev, reps=20):
         "algorithmic_bytes": read + out_thr,
         "with_indices_ms": round(t_idx * 1e3, 4),
         "with_indices_GB_per_s": round((read + out_idx) / t_idx / 1e9, 1),
+        "with_indices_frac": round((read + out_idx) / t_idx / 1e9 / PEAK_HBM_GBS, 4),
+        "with_mask_ms": round(t_mask * 1e3, 4),
+        "with_mask_GB_per_s": round((read + out_mask) / t_mask / 1e9, 1),
+        "with_mask_frac": round((read + out_mask) / t_mask / 1e9 / PEAK_HBM_GBS, 4),
+        "with_mask_note": "thresholds plus the selection bitmask in one pass "
+                          "(topk_threshold_mask, the select the config-4 split forward runs); "
+                          f"{out_mask - out_thr:.0f} bytes of bitmask words written",
         "peak_GB_per_s": PEAK_HBM_GBS,
     }
     del scores
@@ -542,6 +568,7 @@ def cpu_baseline(dev=None, budget_s=12.0):
                           "sample": "config-1 scores [16,512,512], k=32", "cores": cores,
                           "avx512": "avx512f" in native.cpu_flags()}
     res.update(cpu_baseline_wide(cores))
+    res.update(cpu_baseline_small(cores))
     if dev is not None:
         # The reference's hybrid path (dsa_hybrid.py:46-66) on this host: the
         # score matrix crosses PCIe to pinned memory, the CPU selects, the
@@ -640,6 +667,83 @@ def cpu_baseline_wide(cores, budget_s=4.0):
     return out
 
 
+# The reference's published standalone CPU top-K table (README.md:63-67;
+# shapes from bench_avx512.py:55-70, rows N(0,1)), on its Ryzen 9 9950X3D:
+# (B, T, k, torch.topk ms, avx512 ms).
+README_TOPK = ((1, 128, 8, 0.026, 0.005), (4, 128, 8, 0.251, 0.007), (1, 256, 16, 0.189, 0.008),
+               (16, 1024, 64, 8.395, 6.771), (64, 2048, 128, 150.5, 143.9))
+
+
+def time_reference_cpu(fn, budget_s=1.5, warmup=5, iters=30):
+    """bench_avx512.py:25-31's method (5 warm-up calls, then the mean over 30
+    timed calls, perf_counter), with the timed calls capped to about
+    budget_s of work for the slow shapes (at least 3); ms per call."""
+    t0 = time.perf_counter()
+    fn()
+    one = time.perf_counter() - t0
+    for _ in range(min(warmup, max(1, int(budget_s / 4 / max(one, 1e-9))))):
+        fn()
+    n = max(3, min(iters, int(budget_s / max(one, 1e-9))))
+    t0 = time.perf_counter()
+    for _ in range(n):
+        fn()
+    return (time.perf_counter() - t0) / n * 1e3, n
+
+
+def cpu_baseline_small(cores):
+    """The reference's CPU path at its own small shapes:
+      * the torch-vectorised fp32 forward (oracle restatement of
+        dsa_attention_torch, dsa_attention.py:35-52) at configs[0] and at the
+        five config-2 (B, k) shapes, whole forwards;
+      * the standalone k-th largest at the five shapes of the reference's
+        published table: torch.topk's k-th value, the reference's own
+        topk_avx512.cpp (oracle/_ref, when built here) and this repo's host
+        library, beside the published figures."""
+    import torch
+
+    from oracle import dsa_oracle as O
+    from oracle import native
+    from topk_threshold import topk_threshold
+
+    out = {}
+    c0 = dict(B=1, T=128, k=8, HI=4, DI=32, HQ=4, DQ=32, DV=32)
+    rows = []
+    for name, cfg in [("c0", c0)] + [(f"c2_b{B}_k{k}", dict(C1, B=B, k=k)) for B, k, _ in C2_SWEEP]:
+        ins = O.make_inputs(cfg["B"], cfg["T"], cfg["HI"], cfg["DI"], cfg["HQ"], cfg["DQ"], cfg["DV"])
+        ms, n = time_reference_cpu(lambda: O.dsa_forward(*ins, cfg["k"], acc=torch.float32))
+        rows.append({"config": name, "B": cfg["B"], "T": cfg["T"], "k": cfg["k"],
+                     "ms_per_forward": round(ms, 3),
+                     "query_tokens_per_s": round(cfg["B"] * cfg["T"] / (ms / 1e3), 1),
+                     "timed_calls": n})
+        del ins
+    out["forward_small"] = {"workload": "torch-vectorised fp32 DSA forward (oracle restatement "
+                                        "of dsa_attention_torch) at configs[0] and the config-2 "
+                                        "shapes, whole forwards",
+                            "method": "bench_avx512.py:25-31 (5 warm-up, mean of up to 30 "
+                                      "timed calls, capped to ~1.5 s of work)",
+                            "cores": cores, "kind": "port", "rows": rows}
+    ref = native.ref()
+    trows = []
+    for B, T, k, pub_torch, pub_avx in README_TOPK:
+        x = torch.randn((B, T, T), generator=torch.Generator().manual_seed(T + k))
+        row = {"B": B, "T": T, "k": k, "published_torch_ms": pub_torch,
+               "published_avx512_ms": pub_avx}
+        row["torch_topk_ms"] = round(time_reference_cpu(lambda: x.topk(k, dim=-1)[0][..., -1:])[0], 4)
+        row["host_lib_ms"] = round(time_reference_cpu(lambda: topk_threshold(x, k))[0], 4)
+        if ref is not None:
+            row["reference_build_ms"] = round(time_reference_cpu(lambda: ref.topk_threshold(x, k))[0], 4)
+            row["equal"] = bool(torch.equal(ref.topk_threshold(x, k), topk_threshold(x, k)))
+        trows.append(row)
+        del x
+    out["topk_readme_table"] = {
+        "workload": "standalone k-th largest of [B,T,T] N(0,1) fp32 rows at the reference's "
+                    "published shapes (README.md:63-67, bench_avx512.py:55-70)",
+        "published_on": "Ryzen 9 9950X3D, 16 threads",
+        "kind": "reference" if ref is not None else "port",
+        "cores": cores, "rows": trows}
+    return out
+
+
 def pmc_workload(args, dev):
     """Kernels whose FETCH_SIZE / WRITE_SIZE give the traffic figures: a plain
     copy of known size (256 MiB read + 256 MiB written) first, so each
@@ -710,6 +814,11 @@ def main():
                     help="run only the headline leg (fused config 1: warm-up, the timed "
                          "graph and the event-timed launches) and print its JSON line; "
                          "for a kernel-trace profile of that kernel alone")
+    ap.add_argument("--only-select", action="store_true",
+                    help="run only the config-4 select leg (thresholds, thresholds + "
+                         "indices, thresholds + bitmask; then the config-2 standalone "
+                         "top-K) and print its JSON; for a kernel-trace profile of the "
+                         "select kernels alone")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run only the workload profiled with counters: one 256 MiB "
                          "device-to-device copy (counter calibration), then --steps eager "
@@ -729,6 +838,10 @@ def main():
     dev = torch.device("cuda:0")
     if args.pmc_workload:
         pmc_workload(args, dev)
+        return
+    if args.only_select:
+        log("bench: select at config 4 (only)")
+        print(json.dumps({"topk_select": bench_select_c4(dev)}), flush=True)
         return
     B, T = C1["B"], C1["T"]
     log("bench: fused config 1")
@@ -765,6 +878,11 @@ def main():
                      "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 5),
                      "traffic": traffic_from_profile(),
+                     "traffic_source": "profiles/fused_c1_traffic.json: FETCH_SIZE and "
+                                       "WRITE_SIZE of the fused launch in a rocprofv3 --pmc "
+                                       "run of bench.py --pmc-workload, calibrated against a "
+                                       "256 MiB copy in the same run (read from that file, "
+                                       "not measured by this run)",
                      "kernel": "fused_kernel<F32,32,2,2,2,16>",
                      "kernel_ms": round(kern_s * 1e3, 5),
                      "flops_per_launch": flops},

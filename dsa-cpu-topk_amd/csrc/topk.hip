@@ -814,13 +814,16 @@ constexpr int kFinGather = 64;   // kept values of one finishing bin ranked in r
 // IDX (rows of at most 16 chunks): the exactly-k index set too, from the
 // same single read of the row.  While streaming, each thread records which
 // of its entries lie above the interval (certainly selected: abv, bit 4j+c
-// for position (j*NT+tid)*4+c) and which it kept (kpt, in the order it
-// streamed them, the order of its kept values).  Once the threshold is
-// known, each thread sorts its kept values into above / equal to it; the
-// flags go to LDS bitmaps in position order, and one block-wide scan over
-// 64-position ranges places every selected entry at #(above before it) +
-// min(#(equal before it), k - #above), ascending positions -- emit_indices'
-// rule without a pass per chunk.
+// for position (j*NT+tid)*4+c) and which it kept (kpt, same bit order).
+// Its kept values sit in its column in streaming order: the sample chunks'
+// first, then the other chunks', each group in position order, so the s-th
+// kept value is the s-th set bit of kpt over the sample chunks' nibbles,
+// then over the rest.  Once the threshold is known, each thread sorts its
+// kept values into above / equal to it; the flags go to an LDS bitmap in
+// position order, and one block-wide scan over 64-position ranges places
+// every selected entry at #(above before it) + min(#(equal before it), k -
+// #above), ascending positions -- emit_indices' rule without a pass per
+// chunk.  MASK (the same rows): the bitmap's words are the bitmask.
 template <int NT, bool IDX, bool MASK = false>
 __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
   // IDX: exactly-k indices; MASK: the selection bitmask (a.mask), both from
@@ -972,27 +975,32 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
   bool bad = false;            // wave-uniform: a column came near CAP
   uint32_t* col = lds + tid;
   uint64_t abv = 0, kpt = 0;   // FLAGS: entries above the interval; kept entries
-  // Returns bit 0: kept, bit 1: above the interval (NaN included), bit 2: NaN.
-  auto take = [&](float v, bool valid) -> uint32_t {
+  // Streams one value: counts it below fhi, keeps it in the column if in
+  // [flo, fhi).  FLAGS: kp = kept; ab = above the interval -- indices rank
+  // NaN first (torch.topk's order), so for them every valid value not below
+  // fhi; the bitmask selects by score >= thr, which no NaN passes, so for it
+  // the values >= fhi.  Each flag is one compare (or one reused) and a
+  // select of its bit in record(), not a packed code unpacked again.
+  struct Took {
+    bool kp, ab;
+  };
+  auto take = [&](float v, bool valid) -> Took {
     const bool lt = valid && v < fhi;
     const bool kp = lt && !(v < flo);
     col[kc * NT] = __float_as_uint(v);  // the next free slot; kept only if kc advances
     below += lt ? 1u : 0u;
     kc += kp ? 1u : 0u;
-    return (kp ? 1u : 0u) | ((valid && !lt) ? 2u : 0u) | ((valid && v != v) ? 4u : 0u);
+    return Took{kp, MASK ? (valid && v >= fhi) : (valid && !lt)};
   };
-  // FLAGS: a chunk's 4 results into the masks (chunk j, streaming slot sl).
-  // Indices rank NaN first (torch.topk's order); the bitmask selects by
-  // score >= thr, which no NaN passes, so MASK leaves NaN out of "above".
-  auto record = [&](uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3, int j, int sl) {
+  // FLAGS: a chunk's 4 results into the masks (chunk j).
+  auto record = [&](const Took (&r)[4], int j) {
     if constexpr (FLAGS) {
-      auto ab = [](uint32_t r) { return MASK ? ((r >> 1) & ~(r >> 2) & 1u) : ((r >> 1) & 1u); };
-      const uint32_t nk = (r0 & 1u) | ((r1 & 1u) << 1) | ((r2 & 1u) << 2) | ((r3 & 1u) << 3);
-      const uint32_t na = ab(r0) | (ab(r1) << 1) | (ab(r2) << 2) | (ab(r3) << 3);
+      const uint32_t nk = (r[0].kp ? 1u : 0u) | (r[1].kp ? 2u : 0u) | (r[2].kp ? 4u : 0u) | (r[3].kp ? 8u : 0u);
+      const uint32_t na = (r[0].ab ? 1u : 0u) | (r[1].ab ? 2u : 0u) | (r[2].ab ? 4u : 0u) | (r[3].ab ? 8u : 0u);
       abv |= static_cast<uint64_t>(na) << (4 * j);
-      kpt |= static_cast<uint64_t>(nk) << (4 * sl);
+      kpt |= static_cast<uint64_t>(nk) << (4 * j);
     } else {
-      (void)r0; (void)r1; (void)r2; (void)r3; (void)j; (void)sl;
+      (void)r; (void)j;
     }
   };
   // Before every 4 values: a column with fewer than 4 free slots stops the
@@ -1004,10 +1012,10 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     if (room()) {
-      uint32_t r[4];
+      Took r[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c) r[c] = take(sv[4 * s + c], !whole || sample_in(4 * s + c));
-      record(r[0], r[1], r[2], r[3], sample_chunk(s), s);
+      record(r, sample_chunk(s));
     }
   }
 
@@ -1041,7 +1049,7 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
       for (int q = 0; q < 4; ++q) {
         const float fv[4] = {cur[q].x, cur[q].y, cur[q].z, cur[q].w};
         if (4 * it + q < ns && room()) {  // else a repeated load past the last chunk
-          uint32_t r[4];
+          Took r[4];
           if ((jc[q] + 1) * CH <= nv) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) r[c] = take(fv[c], true);
@@ -1050,7 +1058,7 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) r[c] = take(fv[c], p0 + c < nv);
           }
-          record(r[0], r[1], r[2], r[3], jc[q], 4 + 4 * it + q);
+          record(r, jc[q]);
         }
       }
 #pragma unroll
@@ -1092,12 +1100,7 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
     // FLAGS: the row's flags as an LDS bitmap in position order, past what
     // the finishing wave uses: byte j*NT+t holds positions (j*NT+t)*4 .. +3,
     // above the threshold in the low nibble, equal to it in the high one.
-    // The values above the interval go in now, while wave 0 finishes.
     uint8_t* fb = reinterpret_cast<uint8_t*>(lds + kIdxMapWord);
-    if constexpr (FLAGS) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) fb[j * NT + tid] = static_cast<uint8_t>((abv >> (4 * j)) & 15u);
-    }
     block_sync_lds();
     if (wid == 0) {  // one wave finishes on the kept list
       const uint32_t krem = ku - tot_above;
@@ -1185,18 +1188,28 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
     if constexpr (FLAGS) {
       block_sync_lds();
       const float thr = rsh[0];
-      // This thread's kept values (its kc entries of the kept list, in its
-      // streaming order) above / equal to thr, into its own bytes.
-      uint64_t rem = kpt;
+      // This thread's kept values (its kc entries of the kept list) above /
+      // equal to thr: the s-th is the s-th set bit of kpt over the sample
+      // chunks' nibbles, then over the other chunks'.
+      uint64_t smask = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) smask |= uint64_t{15} << (4 * sample_chunk(q));
+      uint64_t rem = kpt & smask, rest = kpt & ~smask;
+      uint64_t gt = abv, eq = 0;
       for (uint32_t s = 0; s < kc; ++s) {
-        const int bp = static_cast<int>(__builtin_ctzll(rem));
-        rem &= rem - 1u;
-        const int sl = bp >> 2;
-        const int j = sl < 4 ? sample_chunk(sl) : chunk_of(sl - 4);
+        if (rem == 0u) {
+          rem = rest;
+          rest = 0u;
+        }
+        const uint64_t bit = rem & (0u - rem);
+        rem ^= bit;
         const float v = __uint_as_float(lds[kbase + s]);
-        const uint32_t f = ((v > thr) ? 1u : 0u) | ((v == thr) ? 16u : 0u);
-        fb[j * NT + tid] = static_cast<uint8_t>(fb[j * NT + tid] | (f << (bp & 3)));
+        gt |= v > thr ? bit : 0u;
+        eq |= v == thr ? bit : 0u;
       }
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        fb[j * NT + tid] = static_cast<uint8_t>(((gt >> (4 * j)) & 15u) | (((eq >> (4 * j)) & 15u) << 4));
       block_sync_lds();
       // Thread t takes positions [64t, 64t+64): one scan of its (above,
       // equal) counts places them, and it walks its set bits only.  The k
