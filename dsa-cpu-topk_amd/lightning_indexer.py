@@ -188,14 +188,19 @@ class _ProjectionWeightCache:
 def fuse_projection_weights(W_Q, W_K, W_W, dtype=None) -> torch.Tensor:
     """[W_Q | W_K | W_W | 0-pad] as one [D, n_pad] matrix in `dtype` (default:
     the weights' common dtype).  The zero columns pad each row of the
-    projection output to a 16-byte multiple.  Pass the result as `W_cat` to
-    indexer_from_hidden to skip the per-call cache lookup."""
+    projection output to a 16-byte multiple, and 16-bit weights to a multiple
+    of 256 columns (measured on MI355X at D=2048, HI=64, DI=128 bf16: the
+    GEMM with 8448 columns takes 125.9 us against 133.4 us with 8384; fp32
+    at D=1024, HI=4, DI=32 is faster unpadded, 31.7 against 35.1 us).  Pass
+    the result as `W_cat` to indexer_from_hidden to skip the per-call cache
+    lookup."""
     if dtype is None:
         dtype = L.common_dtype(W_Q, W_K, W_W)
     D = W_Q.shape[0]
     n = W_Q.shape[1] + W_K.shape[1] + W_W.shape[1]
-    per16 = 16 // torch.tensor([], dtype=dtype).element_size()
-    n_pad = (n + per16 - 1) // per16 * per16
+    es = torch.tensor([], dtype=dtype).element_size()
+    per = 256 if es == 2 else 16 // es
+    n_pad = (n + per - 1) // per * per
     wc = torch.zeros(D, n_pad, device=W_Q.device, dtype=dtype)
     wc[:, :n].copy_(torch.cat([W_Q, W_K, W_W], dim=1))
     return wc
