@@ -1101,7 +1101,45 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
     // the finishing wave uses: byte j*NT+t holds positions (j*NT+t)*4 .. +3,
     // above the threshold in the low nibble, equal to it in the high one.
     uint8_t* fb = reinterpret_cast<uint8_t*>(lds + kIdxMapWord);
+    // MASK: before the other waves exit, every thread writes its "above"
+    // bits into the LDS bitmap (byte j*NT+t: positions (j*NT+t)*4 .. +3) and,
+    // next to each of its kept values in the list, that value's bit in the
+    // bitmap; wave 0 then finishes the threshold alone and sets the bits of
+    // the kept values at or above it.  (Waves held at a barrier while wave 0
+    // finishes cost more streaming throughput than wave 0's longer tail:
+    // config 4, 9 us.)  The s-th kept value of a thread is the s-th set bit
+    // of its kept mask over the sample chunks' nibbles, then over the rest.
+    uint16_t* posl = reinterpret_cast<uint16_t*>(lds + kIdxMapWord + 16 * NT / 4);
+    static_assert(!MASK || kIdxMapWord + 16 * NT / 4 + kCandCap / 2 <= CAP * NT, "the bit list fits");
+    if constexpr (MASK) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) fb[j * NT + tid] = static_cast<uint8_t>((abv >> (4 * j)) & 15u);
+      uint64_t smask = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) smask |= uint64_t{15} << (4 * sample_chunk(q));
+      uint64_t rem = kpt & smask, rest = kpt & ~smask;
+      for (uint32_t i = 0; i < kc; ++i) {
+        if (rem == 0u) {
+          rem = rest;
+          rest = 0u;
+        }
+        const int bp = static_cast<int>(__builtin_ctzll(rem));
+        rem &= rem - 1u;
+        // bit (bp & 3) of byte (bp >> 2) * NT + tid
+        posl[kbase + i] = static_cast<uint16_t>(((((bp >> 2) * NT + tid)) << 3) | (bp & 3));
+      }
+    }
     block_sync_lds();
+    if (MASK && wid != 0) return;
+    // nibble `sh` of each of 16 bytes -> 64 bits (the bitmap's 64 positions)
+    auto nib = [](uint4 v, int sh) {
+      auto w16 = [sh](uint32_t w) {
+        w >>= sh;
+        return (w & 0xfu) | ((w >> 4) & 0xf0u) | ((w >> 8) & 0xf00u) | ((w >> 12) & 0xf000u);
+      };
+      return static_cast<uint64_t>(w16(v.x)) | (static_cast<uint64_t>(w16(v.y)) << 16) |
+             (static_cast<uint64_t>(w16(v.z)) << 32) | (static_cast<uint64_t>(w16(v.w)) << 48);
+    };
     if (wid == 0) {  // one wave finishes on the kept list
       const uint32_t krem = ku - tot_above;
       auto visit_kept = [&](auto&& f) {
@@ -1184,8 +1222,28 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
         a.thr[row] = res + 0.0f;  // -0 reported as +0, as the key order does
         rsh[0] = res + 0.0f;
       }
+      if constexpr (MASK) {
+        // the kept values at or above thr set their bits
+        const float thr = res + 0.0f;
+        uint32_t* fbw = reinterpret_cast<uint32_t*>(fb);
+        for (uint32_t i = lane; i < ktot; i += kWave) {
+          if (__uint_as_float(lds[i]) >= thr) {
+            const uint32_t pb = posl[i];
+            atomicOr(&fbw[pb >> 5], 1u << (pb & 31u));
+          }
+        }
+        wave_lds_sync();
+        // words past the row hold no flags, so the words up to the end of
+        // the row's 128-query block are 0 there
+        const int nw = min(static_cast<int>((a.causal_T + 63) / 64), (((nv - 1) | 127) >> 6) + 1);
+#pragma unroll
+        for (int q = 0; q < NW; ++q) {
+          const int w = lane + kWave * q;
+          if (w < nw) a.mask[row * a.ldm + w] = nib(reinterpret_cast<const uint4*>(fb)[w], 0);
+        }
+      }
     }  // wave 0
-    if constexpr (FLAGS) {
+    if constexpr (IDX) {
       block_sync_lds();
       const float thr = rsh[0];
       // This thread's kept values (its kc entries of the kept list) above /
@@ -1215,22 +1273,8 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
       // equal) counts places them, and it walks its set bits only.  The k
       // indices are staged in LDS and written out coalesced.
       const uint4 fv = reinterpret_cast<const uint4*>(fb)[tid];
-      auto nib = [](uint4 v, int sh) {  // nibble `sh` of 16 bytes -> 64 bits
-        auto w16 = [sh](uint32_t w) {
-          w >>= sh;
-          return (w & 0xfu) | ((w >> 4) & 0xf0u) | ((w >> 8) & 0xf00u) | ((w >> 12) & 0xf000u);
-        };
-        return static_cast<uint64_t>(w16(v.x)) | (static_cast<uint64_t>(w16(v.y)) << 16) |
-               (static_cast<uint64_t>(w16(v.z)) << 32) | (static_cast<uint64_t>(w16(v.w)) << 48);
-      };
       const uint64_t G = nib(fv, 0), Eq = nib(fv, 4);
-      if constexpr (MASK) {
-        // Word tid of the row's selection bitmask: positions 64 tid .. +63
-        // at or above thr.  Positions past the row hold no flags, so the
-        // words up to the end of the row's 128-query block are 0 there.
-        const int nw = min(static_cast<int>((a.causal_T + 63) / 64), (((nv - 1) | 127) >> 6) + 1);
-        if (tid < nw) a.mask[row * a.ldm + tid] = G | Eq;
-      } else {
+      {
         uint32_t tot;
         const uint32_t ex = block_exclusive_sum<NT>(
             static_cast<uint32_t>(__builtin_popcountll(G)) |
