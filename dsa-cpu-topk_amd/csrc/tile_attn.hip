@@ -197,6 +197,11 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
   // DMA into one buffer does not alias reads of the other, and keeps the
   // next tile's DMA in flight while the current tile is read.
   __shared__ __align__(16) uint8_t k0[L::BYTES], k1[L::BYTES], v0[L::BYTES], v1[L::BYTES];
+  // Bitmask form: the bias of the four keys one nibble of a mask word
+  // covers, entry n = {bit r of n set ? 0 : -inf, r = 0..3} (256 bytes).
+  // The S accumulators start from it, so an unselected key's logit leaves
+  // the MFMA as -inf + logit and a selected one as +0 + logit.
+  __shared__ __align__(16) float btab[MASK ? 64 : 4];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS targets in SGPRs
@@ -204,6 +209,10 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
   const int g = lane >> 4, c16 = lane & 15;
   const int T = a.T;
   const int HQ = a.HQ;
+  if constexpr (MASK) {  // published by the barrier before the first tile
+    if (tid < 64) btab[tid] = (((tid >> 2) >> (tid & 3)) & 1) ? 0.f : -__builtin_huge_valf();
+  }
+  const DSA_LDS uint8_t* const btabl = (const DSA_LDS uint8_t*)btab;
 
   // Block -> (tile, batch, head): tiles longest first, then batch, head fastest.
   const int ntile = (T + kTQ - 1) / kTQ;
@@ -394,6 +403,20 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
     // products (a scheduling fence keeps them together), so one LDS latency
     // is paid per half tile instead of one per fragment.
     f32x4 st[4][2];
+    if constexpr (MASK) {
+      // entry (j, r) of lane group g is bit 16j + r of the word shifted
+      // right by 4g: nibble j of it indexes the bias table
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        const uint64_t w = mwc[qt] >> (4 * g);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t h = static_cast<uint32_t>(w >> (32 * (j >> 1)));
+          const uint32_t nib = (h >> (16 * (j & 1))) & 15u;
+          st[j][qt] = *reinterpret_cast<const DSA_LDS f32x4*>(btabl + 16 * nib);
+        }
+      }
+    }
 #pragma unroll
     for (int jp = 0; jp < 4; jp += KJ) {
       u32x4 ka[KJ][NKS];
@@ -405,8 +428,10 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int jj = 0; jj < KJ; ++jj) {
+        if constexpr (!MASK) {
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) st[jp + jj][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int qt = 0; qt < 2; ++qt) st[jp + jj][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
@@ -422,33 +447,66 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
     u32x4 pf[2][2];
     bool grow = false;
     float alpha[2];
+    // Bitmask form: the entries hold the logit where selected and -inf +
+    // logit where not, which is -inf unless the logit is +inf or NaN (a
+    // non-finite Q or K row).  The tile max per lane is NaN-propagating
+    // (v_maximum3), so such an entry, or a selected NaN logit, shows; the
+    // wave then masks its entries exactly (the logit where selected, -inf
+    // where not) and takes the max that ignores NaN, as the scores form
+    // does.  Without NaN both maxima agree, so either way the result is
+    // that of exact masking.
+    float mxm[2];
+    if constexpr (MASK) {
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        mxm[qt] = -__builtin_huge_valf();
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mxm[qt] = __builtin_elementwise_maximum(mxm[qt], st[j][qt][r]);
+      }
+      if (__ballot(__builtin_isnan(mxm[0]) | __builtin_isnan(mxm[1])) != 0) {
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              // bit 16j + r of the word shifted right by 4g: a sign-extended
+              // bit field (0 or ~0) and a bit select of the logit or -inf.
+              // Scalars move between float and integer through
+              // __float_as_uint / __uint_as_float: this toolchain
+              // miscompiles __builtin_bit_cast of a vector element (every
+              // element then reads element 0).
+              const uint32_t hw = static_cast<uint32_t>((mwc[qt] >> (4 * g)) >> (32 * (j >> 1)));
+              const uint32_t keep =
+                  static_cast<uint32_t>(static_cast<int32_t>(hw << (31 - (16 * (j & 1) + r))) >> 31);
+              const float x = st[j][qt][r];
+              st[j][qt][r] = __uint_as_float((__float_as_uint(x) & keep) | (0xff800000u & ~keep));
+            }
+          mxm[qt] = -__builtin_huge_valf();
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mxm[qt] = fmaxf(mxm[qt], st[j][qt][r]);
+        }
+      }
+    }
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-      // masked logits: the logit where selected, -inf where not
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if constexpr (MASK) {
-            // entry (j, r) of lane group g is bit 16j + r of the word shifted
-            // right by 4g: a sign-extended bit field (0 or ~0) and a bit
-            // select of the logit or -inf, two VALU instructions.  Scalars
-            // move between float and integer through __float_as_uint /
-            // __uint_as_float: this toolchain miscompiles __builtin_bit_cast
-            // of a vector element (every element then reads element 0).
-            const uint32_t hw = static_cast<uint32_t>((mwc[qt] >> (4 * g)) >> (32 * (j >> 1)));
-            const uint32_t keep =
-                static_cast<uint32_t>(static_cast<int32_t>(hw << (31 - (16 * (j & 1) + r))) >> 31);
-            const float x = st[j][qt][r];
-            st[j][qt][r] = __uint_as_float((__float_as_uint(x) & keep) | (0xff800000u & ~keep));
-          } else {
-            st[j][qt][r] = sel[qt][j][r] ? st[j][qt][r] : -__builtin_huge_valf();
-          }
       float mx = -__builtin_huge_valf();
+      if constexpr (MASK) {
+        mx = mxm[qt];
+      } else {
+        // masked logits: the logit where selected, -inf where not
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[j][qt][r]);
+          for (int r = 0; r < 4; ++r) {
+            st[j][qt][r] = sel[qt][j][r] ? st[j][qt][r] : -__builtin_huge_valf();
+            mx = fmaxf(mx, st[j][qt][r]);
+          }
+      }
       mx = max_xor32(max_xor16(mx));  // over the 4 lane groups (VALU lane swaps)
       const float m_blk = mx * a.scale_log2;
       const bool up = m_blk > m[qt] + 8.f;

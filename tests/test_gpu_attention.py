@@ -227,6 +227,36 @@ def test_mask_kernel_equals_tiled(dev, B, T, HQ, D, k, dtype):
     assert torch.equal(out, ref)
 
 
+@pytest.mark.parametrize("T,D", [(300, 64), (700, 128)])
+def test_mask_kernel_nonfinite_logits(dev, T, D):
+    """K rows with +inf, -inf or NaN elements and a Q row with +inf give
+    non-finite logits.  Unselected keys' logits are masked to -inf whatever
+    they are, as the reference masks them before its softmax; selected ones
+    make the row NaN where the reference's does.  The bitmask path (whose
+    S accumulators start from 0 / -inf biases and re-mask exactly when a NaN
+    shows) equals the scores-reading tile kernel bit for bit, NaN positions
+    included, and the oracle's NaN positions and values elsewhere."""
+    B, HQ, k = 1, 2, 40
+    _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, HQ, D, D, dtype=BF, seed0=4)
+    g = torch.Generator().manual_seed(23)
+    rows = torch.randperm(T, generator=g)[:12].tolist()
+    for i, r in enumerate(rows):
+        K[0, r, i % HQ, (7 * i) % D] = (math.inf, -math.inf, math.nan)[i % 3]
+    Q[0, T // 3, 1, 3] = math.inf
+    s = torch.randn(B, T, T, generator=g)
+    thr = kth(k)(s)
+    args = (Q.to(dev), K.to(dev), V.to(dev))
+    out = sparse_attention_hip(s.to(dev), thr.to(dev), *args, kernel="mask").cpu()
+    ref = sparse_attention_hip(s.to(dev), thr.to(dev), *args, kernel="tiled").cpu()
+    nan = torch.isnan(ref)
+    assert torch.equal(torch.isnan(out), nan)
+    assert torch.equal(out.nan_to_num(0.0), ref.nan_to_num(0.0))
+    want = O.sparse_attn_threshold(s, thr, Q, K, V)
+    assert torch.equal(nan, torch.isnan(want))
+    assert 0 < int(nan.sum()) < nan.numel()
+    assert close(out[~nan], want[~nan], 2e-2, 2e-2)[0]
+
+
 def test_mask_kernel_empty_rows_and_dense(dev):
     """NaN / +inf thresholds give NaN rows; -inf selects every causal key."""
     B, T, HQ, D = 1, 300, 2, 64
