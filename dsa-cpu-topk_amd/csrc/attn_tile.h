@@ -26,6 +26,43 @@ namespace dsa {
 
 constexpr int kListCap = 512;  // one 512-entry segment of the score row
 
+// The keys s0 .. min(s0 + kListCap, t + 1) - 1 whose score is >= thr (a NaN
+// score or threshold selects nothing), in index order, into `list`; returns
+// how many (wave-uniform).  Lane l scans entries s0 + 8l .. s0 + 8l + 7 (two
+// float4 through load4) and the lanes' counts are placed by a wave prefix
+// sum.  The caller syncs the wave's LDS before reading the list.
+template <typename Load4>
+__device__ __forceinline__ int compact_segment(int s0, int t, float thr, Load4& load4, int* list) {
+  const int lane = lane_id();
+  const int sb = s0 + 8 * lane;
+  float sv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (sb <= t) {
+    float a4[4];
+    load4(sb, a4);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) sv[c] = a4[c];
+    if (sb + 4 <= t) {
+      load4(sb + 4, a4);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) sv[4 + c] = a4[c];
+    }
+  }
+  int cnt = 0;
+  bool keep[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    keep[c] = (sb + c <= t) && (sv[c] >= thr);
+    cnt += keep[c] ? 1 : 0;
+  }
+  const int incl = wave_inclusive_sum(cnt);
+  const int total = wave_read_lane(incl, kWave - 1);
+  int p = incl - cnt;
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+    if (keep[c]) list[p++] = sb + c;
+  return total;
+}
+
 // This lane's slice of query row t, times scale_log2 (0 past the row).
 // EQ: elements the wave covers (its heads times DQ); RQ: elements from one
 // query row to the next (EQ, or HQ*DQ when the wave covers a head chunk).
@@ -307,33 +344,7 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
   };
 
   for (int s0 = 0; s0 <= t; s0 += kListCap) {
-    // Lane l scans entries s0 + 8l .. s0 + 8l + 7 (two float4).
-    const int sb = s0 + 8 * lane;
-    float sv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (sb <= t) {
-      float a4[4];
-      load4(sb, a4);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) sv[c] = a4[c];
-      if (sb + 4 <= t) {
-        load4(sb + 4, a4);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) sv[4 + c] = a4[c];
-      }
-    }
-    int cnt = 0;
-    bool keep[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      keep[c] = (sb + c <= t) && (sv[c] >= thr);
-      cnt += keep[c] ? 1 : 0;
-    }
-    const int incl = wave_inclusive_sum(cnt);
-    const int total = wave_read_lane(incl, kWave - 1);
-    int p = incl - cnt;
-#pragma unroll
-    for (int c = 0; c < 8; ++c)
-      if (keep[c]) list[p++] = sb + c;
+    const int total = compact_segment(s0, t, thr, load4, list);
     wave_lds_sync();
     if (use_rs) run_groups(total, half_a_rs, half_b_rs);
     else run_groups(total, half_a, half_b);
@@ -352,6 +363,157 @@ __device__ __forceinline__ void attend_query(const typename Tag::raw* __restrict
     const float inv = 1.f / lsum;  // lsum == 0 only if nothing passed: NaN, as the reference
 #pragma unroll
     for (int e = 0; e < EV; ++e) out_row[lane * EV + e] = acc[e] * inv;
+  }
+}
+
+// Elements [4j, 4j + 4), j = lane % 32, of fp32 query row t (rows of 128
+// elements), times scale_log2: attend_query_pair's slice.
+__device__ __forceinline__ void load_query_pair(const float* __restrict__ Q, int t, float scale_log2,
+                                                float (&q)[4]) {
+  const float4 f =
+      *reinterpret_cast<const float4*>(Q + static_cast<int64_t>(t) * 128 + 4 * (lane_id() & 31));
+  q[0] = f.x * scale_log2;
+  q[1] = f.y * scale_log2;
+  q[2] = f.z * scale_log2;
+  q[3] = f.w * scale_log2;
+}
+
+// attend_query for fp32 rows of exactly 128 elements (HQ*DQ = HQ*DV = 128,
+// DQ = DV, DQ % 4 == 0; Q, K, V and out 16-byte aligned), two keys per gather
+// instruction.  Lane l owns elements [4j, 4j + 4), j = l % 32, of a row; in
+// load i of a group the lower half-wave reads key 2i of the group and the
+// upper half key 2i + 1, so one wave load moves 16 bytes per lane (two
+// 512-byte rows) where attend_query moves 8 (one row).  A CU issues random-row
+// gathers at about one wave load per 15 cycles whatever their width up to 16
+// bytes per lane (a probe of L2-resident random rows on gfx950: ~35 bytes per
+// cycle per CU with 8-byte lanes, ~62 with 16-byte lanes), so two rows per
+// load halve the gather instructions.  A head spans DQ/4 lanes of a half and
+// its logit is a butterfly over them.  The running max is shared by the two
+// halves (one lane exchange per group of 16 keys); each half sums the
+// probabilities and P*V of the keys it read, and the halves' sums are added
+// at the end.  Same selection and result as attend_query (the sums are
+// ordered differently: rounding differs at the last bits).  A group's K and
+// V loads go out together (overlapping them with the neighbouring group's
+// arithmetic, as attend_query's PIPE form does, measured 2% slower here: the
+// gathers are bound by the CU's load issue, not by their latency).
+template <typename Load4>
+__device__ __forceinline__ void attend_query_pair(const float* __restrict__ Q,
+                                                  const float* __restrict__ K,
+                                                  const float* __restrict__ V, int t, int DQ,
+                                                  float scale_log2, float thr, Load4&& load4,
+                                                  int* list, float* __restrict__ out_row,
+                                                  const float* qpre = nullptr) {
+  constexpr uint32_t kRowBytes = 128 * 4;
+  constexpr int NL = 8;  // loads per group: 16 keys
+  const int lane = lane_id();
+  const int half = lane >> 5;
+  const int j4 = 4 * (lane & 31);
+  const int lph = DQ / 4;  // lanes per head
+  float q[4];
+  if (qpre != nullptr) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q[e] = qpre[e];
+  } else {
+    load_query_pair(Q, t, scale_log2, q);
+  }
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float m = -__builtin_huge_valf();
+  float lsum = 0.f;
+  const uint32_t off_l = static_cast<uint32_t>(j4) * 4u;
+  const char* Kb = reinterpret_cast<const char*>(K);
+  const char* Vb = reinterpret_cast<const char*>(V);
+  // Load i reads key 2i + half of the group's list entries ss[0..nu); entries
+  // past nu read key ss[0] and are masked (ok = false).  The list comes in
+  // with vector LDS reads (every lane the same 16 entries); every load takes
+  // a 32-bit byte offset against the uniform base (the host keeps a batch
+  // element's K and V under 4 GiB).
+  auto load_rows = [&](const char* base, const int* ss, int nu, float (&r)[NL][4],
+                       bool (&ok)[NL]) {
+    int raw_idx[2 * NL];
+#pragma unroll
+    for (int i = 0; i < NL / 2; ++i) {
+      const int4 v4 = reinterpret_cast<const int4*>(ss)[i];
+      raw_idx[4 * i] = v4.x; raw_idx[4 * i + 1] = v4.y; raw_idx[4 * i + 2] = v4.z; raw_idx[4 * i + 3] = v4.w;
+    }
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      ok[i] = 2 * i + half < nu;
+      const int s = half ? raw_idx[2 * i + 1] : raw_idx[2 * i];
+      const uint32_t sidx = static_cast<uint32_t>(ok[i] ? s : raw_idx[0]);
+      const float4 f = *reinterpret_cast<const float4*>(base + (sidx * kRowBytes + off_l));
+      r[i][0] = f.x; r[i][1] = f.y; r[i][2] = f.z; r[i][3] = f.w;
+    }
+  };
+  float lg[NL];
+  // Logits of the group's keys and the softmax rescale (from K).
+  auto half_a = [&](const bool (&ok)[NL], const float (&kv)[NL][4]) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) d = fmaf(q[e], kv[i][e], d);
+      lg[i] = d;
+    }
+    auto head_sum = [&](auto step) {
+      constexpr int W = decltype(step)::value;
+      if (lph > W) {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) lg[i] += dpp_partner<W>(lg[i]);
+      }
+    };
+    head_sum(std::integral_constant<int, 1>{});
+    head_sum(std::integral_constant<int, 2>{});
+    head_sum(std::integral_constant<int, 4>{});
+    head_sum(std::integral_constant<int, 8>{});
+    if (lph > 16) {
+#pragma unroll
+      for (int i = 0; i < NL; ++i) lg[i] = sum_xor16(lg[i]);
+    }
+    float mx = -__builtin_huge_valf();
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      lg[i] = ok[i] ? lg[i] : -__builtin_huge_valf();
+      mx = fmaxf(mx, lg[i]);
+    }
+    const float mnew = fmaxf(m, max_xor32(mx));  // over both halves' keys
+    const float alpha = exp2f(m - mnew);
+    lsum *= alpha;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] *= alpha;
+    m = mnew;
+  };
+  // P*V of the group's keys (from V).
+  auto half_b = [&](const bool (&ok)[NL], const float (&vv)[NL][4]) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      // bare v_exp_f32: results below 2^-126 flush to 0, which no sum can see
+      const float p = ok[i] ? __builtin_amdgcn_exp2f(lg[i] - m) : 0.f;
+      lsum += p;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = fmaf(p, vv[i][e], acc[e]);
+    }
+  };
+  float kv[NL][4], vv[NL][4];
+  bool okk[NL], okv[NL];
+  for (int s0 = 0; s0 <= t; s0 += kListCap) {
+    const int total = compact_segment(s0, t, thr, load4, list);
+    wave_lds_sync();
+    for (int i = 0; i < total; i += 2 * NL) {
+      const int nu = min(2 * NL, total - i);
+      load_rows(Kb, list + i, nu, kv, okk);
+      load_rows(Vb, list + i, nu, vv, okv);
+      half_a(okk, kv);
+      half_b(okv, vv);
+    }
+    wave_lds_sync();
+  }
+  lsum = sum_xor32(lsum);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) acc[e] = sum_xor32(acc[e]);
+  if (half == 0) {
+    const float inv = 1.f / lsum;  // lsum == 0 only if nothing passed: NaN, as the reference
+    *reinterpret_cast<float4*>(out_row + j4) =
+        make_float4(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
   }
 }
 

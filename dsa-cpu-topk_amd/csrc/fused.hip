@@ -83,9 +83,13 @@ size_t fused_lds_bytes(int T, int QB) {
 // whole grid of a T = 512 problem is then resident at once.
 // QB queries per block (16, or 8 when 16-query blocks would leave CUs idle):
 // each wave finishes QB/8 rows.
-template <typename Tag, int DI, int KB, int EK, int EV, int QB>
+// PAIR: fp32 attention rows of 128 elements gathered two keys per wave load
+// (attend_query_pair); the host takes it when DQ % 4 == 0 and Q, K, V and
+// out are 16-byte aligned.
+template <typename Tag, int DI, int KB, int EK, int EV, int QB, bool PAIR>
 __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kernel(FusedArgs a) {
   static_assert(QB == 8 || QB == 16, "8 or 16 queries per block");
+  static_assert(!PAIR || (std::is_same_v<Tag, F32> && EK == 2 && EV == 2), "rows of 128 fp32");
   constexpr int RPW = QB / kFusedWaves;  // rows per wave
   using raw = typename Tag::raw;
   extern __shared__ __align__(16) float smem[];
@@ -196,11 +200,13 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
 
   // 2. rows 2w, 2w+1 of the block.  Both query rows are loaded first, so
   // their latency hides behind the first row's select.
-  float qpre[RPW][EK];
+  constexpr int QE = PAIR ? 4 : EK;  // query elements per lane
+  float qpre[RPW][QE];
 #pragma unroll
   for (int rr = 0; rr < RPW; ++rr) {
     const int t = min(tile * QB + RPW * wave + rr, T - 1);
-    load_query<Tag, EK>(Q, t, static_cast<int>(EQ), a.scale_log2, qpre[rr]);
+    if constexpr (PAIR) load_query_pair(Q, t, a.scale_log2, qpre[rr]);
+    else load_query<Tag, EK>(Q, t, static_cast<int>(EQ), a.scale_log2, qpre[rr]);
   }
 #pragma unroll
   for (int rr = 0; rr < RPW; ++rr) {
@@ -225,20 +231,23 @@ __global__ __launch_bounds__(64 * kFusedWaves, DI <= 64 ? 4 : 1) void fused_kern
                                                           reinterpret_cast<uint32_t*>(list),
                                                           rlo, rhi, rbad);
     // attention over keys with score >= thr.
-    attend_query<Tag, EK, EV, true>(
-        Q, K, V, t, a.HQ, a.DQ, a.DV, a.scale_log2, thr,
-        [&](int s, float(&sv)[4]) {
-          const float4 f = *reinterpret_cast<const float4*>(row + s);
-          sv[0] = f.x; sv[1] = f.y; sv[2] = f.z; sv[3] = f.w;
-        },
-        list, a.out + (b * T + t) * EVt, qpre[rr]);
+    auto load4 = [&](int s, float(&sv)[4]) {
+      const float4 f = *reinterpret_cast<const float4*>(row + s);
+      sv[0] = f.x; sv[1] = f.y; sv[2] = f.z; sv[3] = f.w;
+    };
+    if constexpr (PAIR)
+      attend_query_pair(Q, K, V, t, a.DQ, a.scale_log2, thr, load4, list,
+                        a.out + (b * T + t) * EVt, qpre[rr]);
+    else
+      attend_query<Tag, EK, EV, true>(Q, K, V, t, a.HQ, a.DQ, a.DV, a.scale_log2, thr, load4, list,
+                                      a.out + (b * T + t) * EVt, qpre[rr]);
   }
 }
 
-template <typename Tag, int DI, int KB, int EK, int EV, int QB>
+template <typename Tag, int DI, int KB, int EK, int EV, int QB, bool PAIR>
 hipError_t launch(const FusedArgs& a, hipStream_t stream) {
   const size_t lds = fused_lds_bytes(a.T, QB);
-  auto kern = fused_kernel<Tag, DI, KB, EK, EV, QB>;
+  auto kern = fused_kernel<Tag, DI, KB, EK, EV, QB, PAIR>;
   // Raise the dynamic-LDS limit of this instance once, to what T = 2048 needs.
   // A runtime that does not need (or know) the attribute may refuse it; the
   // launch below then reports any real shortfall itself.
@@ -284,19 +293,27 @@ int elems_per_lane(int HQ, int D) {
 
 // 16-query blocks unless they would leave compute units idle (fewer blocks
 // than CUs): then 8-query blocks, one row per wave, twice the blocks.
+// pair: fp32 rows of 128 elements may take attend_query_pair.
 template <typename Tag, int DI, int KB, int EK>
-hipError_t launch_qb(const FusedArgs& a, hipStream_t stream) {
+hipError_t launch_qb(const FusedArgs& a, bool pair, hipStream_t stream) {
   const int cus = device_cus();
-  if (cus > 0 && a.B * ((a.T + 15) / 16) < cus) return launch<Tag, DI, KB, EK, EK, 8>(a, stream);
-  return launch<Tag, DI, KB, EK, EK, 16>(a, stream);
+  const bool qb8 = cus > 0 && a.B * ((a.T + 15) / 16) < cus;
+  if constexpr (std::is_same_v<Tag, F32> && EK == 2) {
+    if (pair) {
+      if (qb8) return launch<Tag, DI, KB, EK, EK, 8, true>(a, stream);
+      return launch<Tag, DI, KB, EK, EK, 16, true>(a, stream);
+    }
+  }
+  if (qb8) return launch<Tag, DI, KB, EK, EK, 8, false>(a, stream);
+  return launch<Tag, DI, KB, EK, EK, 16, false>(a, stream);
 }
 
 #define DSA_FUSED_EK(Tag, di, kb)                                              \
   switch (EK) {                                                                \
-    case 1: return launch_qb<Tag, di, kb, 1>(a, stream);                       \
-    case 2: return launch_qb<Tag, di, kb, 2>(a, stream);                       \
-    case 4: return launch_qb<Tag, di, kb, 4>(a, stream);                       \
-    case 8: return launch_qb<Tag, di, kb, 8>(a, stream);                       \
+    case 1: return launch_qb<Tag, di, kb, 1>(a, pair, stream);                 \
+    case 2: return launch_qb<Tag, di, kb, 2>(a, pair, stream);                 \
+    case 4: return launch_qb<Tag, di, kb, 4>(a, pair, stream);                 \
+    case 8: return launch_qb<Tag, di, kb, 8>(a, pair, stream);                 \
   }                                                                            \
   break;
 
@@ -332,6 +349,10 @@ hipError_t launch_fused(const void* qi, const void* ki, const void* wi, const vo
               scale * 1.4426950408889634f, out, row_stride(static_cast<int>(T)), 0};
   const int EK = elems_per_lane(HQ, DQ);
   if (elems_per_lane(HQ, DV) != EK) return hipErrorNotSupported;
+  // Two keys per gather instruction for fp32 rows of 128 elements.
+  const bool pair = dtype == 0 && HQ * DQ == 128 && DQ == DV && DQ % 4 == 0 &&
+                    ((reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(K) |
+                      reinterpret_cast<uintptr_t>(V) | reinterpret_cast<uintptr_t>(out)) & 15u) == 0;
   // Key blocks per indexer super-block (KB): fp32 rows take 2 (config 1:
   // 34.0 us against 35.1 at 4 and 34.4 at 1), DI = 64 takes 1 to stay within
   // 128 VGPRs without scratch.

@@ -40,8 +40,12 @@ struct AttnArgs {
   int nchunk;  // HQ / HQc
 };
 
-template <typename Tag, int EK, int EV>
+// PAIR: fp32 rows of 128 elements gathered two keys per wave load
+// (attend_query_pair); the host takes it for whole rows (no head chunks)
+// with DQ % 4 == 0 and Q, K, V and out 16-byte aligned.
+template <typename Tag, int EK, int EV, bool PAIR = false>
 __global__ __launch_bounds__(256) void sparse_attn_kernel(AttnArgs a) {
+  static_assert(!PAIR || (std::is_same_v<Tag, F32> && EK == 2 && EV == 2), "rows of 128 fp32");
   using raw = typename Tag::raw;
   __shared__ __align__(16) int lists[4][kListCap];
   const int wave = threadIdx.x >> 6;
@@ -64,25 +68,28 @@ __global__ __launch_bounds__(256) void sparse_attn_kernel(AttnArgs a) {
   const float* srow = a.scores + qrow * a.ld;
   const float thr = a.thr[qrow];
   const bool vec = a.vec != 0;
-  attend_query<Tag, EK, EV>(
-      Q, K, V, t, a.HQc, a.DQ, a.DV, a.scale_log2, thr,
-      [&](int s, float(&sv)[4]) {
-        if (vec) {
-          const float4 f = *reinterpret_cast<const float4*>(srow + s);
-          sv[0] = f.x; sv[1] = f.y; sv[2] = f.z; sv[3] = f.w;
-        } else {
+  auto load4 = [&](int s, float(&sv)[4]) {
+    if (vec) {
+      const float4 f = *reinterpret_cast<const float4*>(srow + s);
+      sv[0] = f.x; sv[1] = f.y; sv[2] = f.z; sv[3] = f.w;
+    } else {
 #pragma unroll
-          for (int c = 0; c < 4; ++c) sv[c] = (s + c <= t) ? srow[s + c] : 0.f;
-        }
-      },
-      lists[wave], a.out + qrow * EVt + cv, nullptr, static_cast<int>(EQ),
-      static_cast<int>(EVt));
+      for (int c = 0; c < 4; ++c) sv[c] = (s + c <= t) ? srow[s + c] : 0.f;
+    }
+  };
+  if constexpr (PAIR)
+    attend_query_pair(Q, K, V, t, a.DQ, a.scale_log2, thr, load4, lists[wave],
+                      a.out + qrow * EVt);
+  else
+    attend_query<Tag, EK, EV>(Q, K, V, t, a.HQc, a.DQ, a.DV, a.scale_log2, thr, load4, lists[wave],
+                              a.out + qrow * EVt + cv, nullptr, static_cast<int>(EQ),
+                              static_cast<int>(EVt));
 }
 
-template <typename Tag, int EK, int EV>
+template <typename Tag, int EK, int EV, bool PAIR = false>
 hipError_t launch(const AttnArgs& a, hipStream_t stream) {
   const int64_t nblk = a.B * ((a.T + 3) / 4) * a.nchunk;
-  hipLaunchKernelGGL((sparse_attn_kernel<Tag, EK, EV>), dim3(static_cast<unsigned>(nblk)),
+  hipLaunchKernelGGL((sparse_attn_kernel<Tag, EK, EV, PAIR>), dim3(static_cast<unsigned>(nblk)),
                      dim3(256), 0, stream, a);
   return hipGetLastError();
 }
@@ -173,6 +180,11 @@ hipError_t launch_sparse_attn_gather(const float* scores, int64_t ld, const floa
   AttnArgs a{scores, ld, thr, Q, K, V, B, static_cast<int>(T), HQ, DQ, DV,
              scale * 1.4426950408889634f, out, vec ? 1 : 0, HQc, nchunk};
   const int EK = elems_per_lane(HQc, DQ), EV = elems_per_lane(HQc, DV);
+  // Two keys per gather instruction for whole fp32 rows of 128 elements.
+  if (dtype == 0 && nchunk == 1 && HQ * DQ == 128 && DQ == DV && DQ % 4 == 0 &&
+      ((reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(K) |
+        reinterpret_cast<uintptr_t>(V) | reinterpret_cast<uintptr_t>(out)) & 15u) == 0)
+    return launch<F32, 2, 2, true>(a, stream);
   if (dtype == 0) {
     DSA_ATTN_PAIRS(DSA_ATTN_CASE, F32)
   } else if (dtype == 1) {
