@@ -888,7 +888,7 @@ def main():
                                        "run of bench.py --pmc-workload, calibrated against a "
                                        "256 MiB copy in the same run (read from that file, "
                                        "not measured by this run)",
-                     "kernel": "fused_kernel<F32,32,2,2,2,16>",
+                     "kernel": "fused_kernel<F32,32,2,2,2,16,true>",
                      "kernel_ms": round(kern_s * 1e3, 5),
                      "flops_per_launch": flops},
     }
