@@ -143,8 +143,12 @@ int dsa_topk_threshold(const float* scores, int64_t rows, int64_t n, int64_t ld,
  * computes it on the CPU, dsa_hybrid.py:61-66).
  * Replaces: _sparse_attn_kernel + sparse_attention_with_threshold_triton,
  *           reference dsa_attention.py:234-324.
- * Kernels (chosen by shape, same sel and O): per-query gathers; rows wider
- *   than one wave holds (fp32 HQ*D > 1024, 16-bit > 2048) in head chunks;
+ * Kernels (chosen by shape, same sel and O): per-query gathers (fp32 rows
+ *   of HQ*DQ = 128 elements with Q, K, V and out 16-byte aligned load two
+ *   keys per wave instruction, one per half-wave; the sums then run in
+ *   another order, so results differ from the one-key form in the last
+ *   bits); rows wider than one wave holds (fp32 HQ*D > 1024, 16-bit > 2048)
+ *   in head chunks;
  *   the tile kernel below for 16-bit DQ = DV in {64,128} at T >= 4096 or on
  *   wide rows; the staged kernel below for fp32 rows of HQ*DQ = 512 at
  *   T >= 3072 when the batch gives at least half a block per compute unit.
@@ -287,7 +291,8 @@ int dsa_sparse_attn_uses_mask(int dtype, int64_t T, int HQ, int DQ, int DV);
  * Fused DSA forward for T <= 2048: indexer -> per-row radix select ->
  * sparse attention in one kernel; the score rows live in LDS only.
  * Same result as dsa_indexer_scores + dsa_topk_threshold(k = min(top_k,T),
- * causal) + dsa_sparse_attn_threshold.
+ * causal) + dsa_sparse_attn_threshold (the attention gathers as that entry's
+ * per-query gathers do, two keys per load under the same conditions).
  * Replaces: _dsa_fused_kernel + dsa_attention_triton,
  *           reference dsa_attention.py:96-227.
  * Constraints: 1 <= T <= 2048; 1 <= top_k; the indexer's and the sparse
