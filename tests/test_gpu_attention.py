@@ -52,6 +52,15 @@ def test_kth_threshold(dev, B, T, HQ, D, k):
     run_case(dev, B, T, HQ, D, D, kth(k))
 
 
+@pytest.mark.parametrize("HQ,D", [(32, 4), (16, 8), (8, 16), (4, 32), (2, 64), (1, 128)])
+def test_two_keys_per_load_head_widths(dev, HQ, D):
+    """fp32 rows of HQ*D = 128 elements gather two keys per wave load, each
+    half-wave one key's row; a head spans D/4 lanes of a half (1 to 32: the
+    logit's butterfly is 0 to 5 steps, the last across 16-lane rows).  Every
+    width against the oracle, with ties at the threshold and a ragged T."""
+    run_case(dev, 2, 301, HQ, D, D, kth(40))
+
+
 @pytest.mark.parametrize("HQ,DQ,DV", [(4, 32, 64), (4, 64, 32), (2, 16, 32), (8, 64, 128)])
 def test_dq_ne_dv(dev, HQ, DQ, DV):
     run_case(dev, 2, 160, HQ, DQ, DV, kth(12))

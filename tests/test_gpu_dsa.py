@@ -68,6 +68,24 @@ def test_all_three_agree_small(dev):
     assert np.abs(b - c).max() < 5e-4
 
 
+@pytest.mark.parametrize("HQ,DH", [(32, 4), (16, 8), (8, 16), (2, 64), (1, 128)])
+def test_fused_two_keys_per_load_head_widths(dev, HQ, DH):
+    """The fused forward at every head width of the two-keys-per-load
+    gathers (fp32 rows of HQ*D = 128 elements): against the float64 oracle,
+    and equal to the split forward, whose gather kernel shares the code."""
+    B, T, k = 2, 300, 24
+    ins = O.make_inputs(B, T, 4, 32, HQ, DH, DH)
+    g = to_dev(ins, dev)
+    fused = D.dsa_fused_hip(*g, k)
+    split = D.dsa_split_hip(*g, k)
+    torch.cuda.synchronize()
+    s_gpu = indexer_scores_hip(*g[:3]).cpu().double()
+    want = O.sparse_attn_threshold(s_gpu, O.topk_threshold(s_gpu, k), *ins[3:])
+    ok, err, _ = close(fused.cpu(), want, 1e-4, 1e-4)
+    assert ok, f"fused vs oracle on the GPU's scores: max abs err {err}"
+    assert float((fused - split).abs().max()) <= 1e-6
+
+
 @pytest.mark.parametrize("T,top_k", [(32, 8), (64, 16), (128, 32)])
 def test_split_matches_oracle(dev, T, top_k):
     """test_dsa.py:55-61."""
