@@ -11,7 +11,9 @@
 // so a row gather is a single coalesced wave load.  Per-head logits are a
 // butterfly over the DQ/EK lanes of the head, or, when a head spans exactly
 // as many lanes as a gather group has keys, a reduce-scatter that leaves one
-// key's logit per lane (process_rs).  Softmax is online (running
+// key's logit per lane (half_a_rs).  fp32 rows of 128 elements (8 bytes of a
+// key per lane) take attend_query_pair instead: each half-wave reads one
+// key's row, 16 bytes per lane, two keys per load.  Softmax is online (running
 // max m, normaliser l) in the log2 domain with fp32 state, so the whole
 // selected set is never materialised and any selected count works -- ties at
 // the threshold can select more than k keys (the reference keeps ties).

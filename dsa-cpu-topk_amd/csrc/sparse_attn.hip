@@ -4,7 +4,8 @@
 // (reference dsa_attention.py:234-324) and is the last stage of the split
 // forward and of the precomputed-threshold path (dsa_hybrid.py:66).  The
 // reference loads every K/V row of the prefix and masks; this kernel reads
-// only the score row and the selected K/V rows (attn_tile.h).
+// only the score row and the selected K/V rows (attn_tile.h; fp32 rows of
+// 128 elements two keys per wave load, attend_query_pair).
 //
 // Block = 4 waves = 4 consecutive queries of one batch element.  Blocks run
 // longest query first, spread evenly over the XCDs (causal_block_tile).
