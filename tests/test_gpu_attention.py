@@ -61,6 +61,28 @@ def test_two_keys_per_load_head_widths(dev, HQ, D):
     run_case(dev, 2, 301, HQ, D, D, kth(40))
 
 
+@pytest.mark.parametrize("HQ,D", [(4, 32), (8, 64)])
+def test_gather_empty_selection_rows_are_nan(dev, HQ, D):
+    """Per-query gathers (two keys per load at HQ*D = 128, one at 512): rows
+    whose threshold nothing reaches (+inf, NaN) give 0/0 = NaN, as the
+    reference's softmax over an all -inf row; the other rows match the
+    oracle."""
+    B, T = 2, 200
+    _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, HQ, D, D)
+    s = torch.randn(B, T, T, generator=torch.Generator().manual_seed(6))
+    thr = kth(24)(s)
+    bad = torch.tensor([0, 9, 150, 199])
+    thr[1, bad[:2], 0] = math.inf
+    thr[1, bad[2:], 0] = math.nan
+    out = sparse_attention_hip(s.to(dev), thr.to(dev), Q.to(dev), K.to(dev), V.to(dev)).cpu()
+    assert bool(torch.isnan(out[1, bad]).all())
+    good = torch.ones(B, T, dtype=torch.bool)
+    good[1, bad] = False
+    want = O.sparse_attn_threshold(s, thr, Q, K, V)
+    assert not bool(torch.isnan(out[good]).any())
+    assert close(out[good], want[good], 1e-4, 1e-4)[0]
+
+
 @pytest.mark.parametrize("HQ,DQ,DV", [(4, 32, 64), (4, 64, 32), (2, 16, 32), (8, 64, 128)])
 def test_dq_ne_dv(dev, HQ, DQ, DV):
     run_case(dev, 2, 160, HQ, DQ, DV, kth(12))
