@@ -49,6 +49,11 @@ _SIGNATURES = {
                                          _F, _P, _P], _I),
     "dsa_sparse_attn_threshold_staged": ([_P, _I64, _P, _P, _P, _P, _I, _I64, _I64, _I, _I, _I,
                                           _F, _P, _P], _I),
+    "dsa_sparse_attn_threshold_ws": ([_P, _I64, _P, _P, _P, _P, _I, _I64, _I64, _I, _I, _I, _F,
+                                      _P, _P, _I64, _P], _I),
+    "dsa_sparse_attn_threshold_staged_ws": ([_P, _I64, _P, _P, _P, _P, _I, _I64, _I64, _I, _I,
+                                             _I, _F, _P, _P, _I64, _P], _I),
+    "dsa_sparse_attn_workspace_bytes": ([_I, _I, _I64, _I64, _I, _I, _I, _I64], _I64),
     "dsa_fused_forward": ([_P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I, _I, _I, _I, _I, _I, _F,
                            _P, _P], _I),
     "dsa_selection_mask": ([_P, _I64, _P, _I64, _I64, _P, _I64, _P], _I),

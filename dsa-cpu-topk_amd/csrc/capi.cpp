@@ -174,18 +174,36 @@ int dsa_topk_threshold_mask(const float* scores, int64_t B, int64_t T, int64_t l
                     "dsa_topk_threshold_mask");
 }
 
-int dsa_sparse_attn_threshold(const float* scores, int64_t ld, const float* thr, const void* Q,
-                              const void* K, const void* V, int dtype, int64_t B, int64_t T,
-                              int HQ, int DQ, int DV, float scale, float* out, void* stream) {
+int dsa_sparse_attn_threshold_ws(const float* scores, int64_t ld, const float* thr,
+                                 const void* Q, const void* K, const void* V, int dtype,
+                                 int64_t B, int64_t T, int HQ, int DQ, int DV, float scale,
+                                 float* out, void* workspace, int64_t workspace_bytes,
+                                 void* stream) {
   int rc = check_attn(dtype, B, T, HQ, DQ, DV, Q, K, V, out, "sparse_attn");
   if (rc != DSA_OK) return rc;
   if (ld < T) return fail(DSA_EINVAL, "sparse_attn: ld=%lld < T=%lld", (long long)ld, (long long)T);
   if (!std::isfinite(scale)) return fail(DSA_EINVAL, "sparse_attn: scale must be finite");
+  if (workspace_bytes < 0) return fail(DSA_EINVAL, "sparse_attn: negative workspace size");
   if (B * T == 0) return DSA_OK;
   if (!scores || !thr) return fail(DSA_EINVAL, "sparse_attn: null pointer");
   return hip_status(dsa::launch_sparse_attn(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, DV,
-                                            scale, out, static_cast<hipStream_t>(stream)),
+                                            scale, out, workspace, workspace_bytes,
+                                            static_cast<hipStream_t>(stream)),
                     "dsa_sparse_attn_threshold");
+}
+
+int dsa_sparse_attn_threshold(const float* scores, int64_t ld, const float* thr, const void* Q,
+                              const void* K, const void* V, int dtype, int64_t B, int64_t T,
+                              int HQ, int DQ, int DV, float scale, float* out, void* stream) {
+  return dsa_sparse_attn_threshold_ws(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, DV, scale,
+                                      out, nullptr, 0, stream);
+}
+
+int64_t dsa_sparse_attn_workspace_bytes(int staged, int dtype, int64_t B, int64_t T, int HQ,
+                                        int DQ, int DV, int64_t ld) {
+  if (!dtype_ok(dtype) || B < 0 || T < 0 || T > kMaxElems || HQ < 1 || DQ < 1 || DV < 1 || ld < T)
+    return 0;
+  return dsa::sparse_attn_workspace_bytes(staged != 0, dtype, B, T, HQ, DQ, DV, ld);
 }
 
 int dsa_sparse_attn_threshold_tiled(const float* scores, int64_t ld, const float* thr,
@@ -291,10 +309,11 @@ int dsa_sparse_attn_uses_mask(int dtype, int64_t T, int HQ, int DQ, int DV) {
   return dtype_ok(dtype) && dsa::sparse_attn_uses_tiles(dtype, T, HQ, DQ, DV) ? 1 : 0;
 }
 
-int dsa_sparse_attn_threshold_staged(const float* scores, int64_t ld, const float* thr,
-                                     const void* Q, const void* K, const void* V, int dtype,
-                                     int64_t B, int64_t T, int HQ, int DQ, int DV, float scale,
-                                     float* out, void* stream) {
+int dsa_sparse_attn_threshold_staged_ws(const float* scores, int64_t ld, const float* thr,
+                                        const void* Q, const void* K, const void* V, int dtype,
+                                        int64_t B, int64_t T, int HQ, int DQ, int DV, float scale,
+                                        float* out, void* workspace, int64_t workspace_bytes,
+                                        void* stream) {
   int rc = check_attn(dtype, B, T, HQ, DQ, DV, Q, K, V, out, "sparse_attn_staged");
   if (rc != DSA_OK) return rc;
   if (!dsa::staged_attn_supported(dtype, HQ, DQ, DV))
@@ -303,11 +322,21 @@ int dsa_sparse_attn_threshold_staged(const float* scores, int64_t ld, const floa
   if (!dsa::staged_attn_fits(T, ld))
     return fail(DSA_EUNSUPPORTED, "sparse_attn_staged: T*ld*4 = %lld bytes of scores per batch element, the limit is 2^31 (use dsa_sparse_attn_threshold)", (long long)(T * ld * 4));
   if (!std::isfinite(scale)) return fail(DSA_EINVAL, "sparse_attn_staged: scale must be finite");
+  if (workspace_bytes < 0) return fail(DSA_EINVAL, "sparse_attn_staged: negative workspace size");
   if (B * T == 0) return DSA_OK;
   if (!scores || !thr) return fail(DSA_EINVAL, "sparse_attn_staged: null pointer");
   return hip_status(dsa::launch_staged_attn(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, scale,
-                                            out, static_cast<hipStream_t>(stream)),
+                                            out, workspace, workspace_bytes,
+                                            static_cast<hipStream_t>(stream)),
                     "dsa_sparse_attn_threshold_staged");
+}
+
+int dsa_sparse_attn_threshold_staged(const float* scores, int64_t ld, const float* thr,
+                                     const void* Q, const void* K, const void* V, int dtype,
+                                     int64_t B, int64_t T, int HQ, int DQ, int DV, float scale,
+                                     float* out, void* stream) {
+  return dsa_sparse_attn_threshold_staged_ws(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, DV,
+                                             scale, out, nullptr, 0, stream);
 }
 
 int dsa_fused_forward(const void* q_idx, const void* k_idx, const void* w_idx, const void* Q,

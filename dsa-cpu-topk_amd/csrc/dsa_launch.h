@@ -29,11 +29,18 @@ hipError_t launch_indexer(const void* q, const void* k, const void* w, int dtype
 bool indexer_supported(int dtype, int DI);
 bool indexer_fp8_fits(int HI, int DI);  // the fp8 kernel's 4-query tile fits LDS
 
-// Threshold-driven sparse attention.
+// Threshold-driven sparse attention.  ws / ws_bytes: device workspace for
+// the staged kernel's split tiles (sparse_attn_workspace_bytes; null or too
+// small: the staged kernel runs every tile as one chunk).
 hipError_t launch_sparse_attn(const float* scores, int64_t ld, const float* thr, const void* Q,
                               const void* K, const void* V, int dtype, int64_t B, int64_t T,
-                              int HQ, int DQ, int DV, float scale, float* out,
-                              hipStream_t stream);
+                              int HQ, int DQ, int DV, float scale, float* out, void* ws,
+                              int64_t ws_bytes, hipStream_t stream);
+// Workspace bytes with which launch_sparse_attn (staged = false) or
+// launch_staged_attn (staged = true) splits the staged kernel's long tiles;
+// 0 when that launch uses no workspace for this shape.
+int64_t sparse_attn_workspace_bytes(bool staged, int dtype, int64_t B, int64_t T, int HQ, int DQ,
+                                    int DV, int64_t ld);
 bool sparse_attn_supported(int dtype, int HQ, int DQ, int DV);
 // The per-query gather kernel alone (launch_sparse_attn may pick tiles), and
 // whether it splits a row into head chunks for this shape.
@@ -78,22 +85,44 @@ hipError_t launch_sparse_attn_mask_noalloc(const float* scores, int64_t ld, cons
 constexpr int64_t kStagedMinT = 3072;
 bool staged_attn_supported(int dtype, int HQ, int DQ, int DV);
 // Whether the threshold entry point takes the staged kernel: fp32 rows of
-// 512 elements (E = 8) only, T >= kStagedMinT, and at least half a block per
-// compute unit (a block streams the keys of two 32-query tiles and fills a
-// CU's LDS; with fewer blocks, or for fp32 rows of 256 elements or 16-bit
-// rows, the per-query gathers were faster on MI355X: e.g. 0.15 vs 0.38 ms at
-// B=2, T=4096, HQ=4, D=64, k=256 fp32; 0.37 vs 0.41 at B=2, T=4096, HQ=8,
-// D=64, k=256; 0.70 vs 0.44 for the staged kernel at B=4).
-bool staged_attn_auto(int dtype, int64_t B, int64_t T, int HQ, int DQ, int DV);
+// 512 elements (E = 8) only, T >= kStagedMinT, and either a workspace for
+// split key ranges (`split`) or at least half a block of tile pairs per
+// compute unit.  For fp32 rows of 256 elements and 16-bit rows the per-query
+// gathers measured faster on MI355X (B=2, T=4096, HQ=4, D=64, k=256: 0.17
+// against 0.30 ms split; bf16 HQ=8 at T=3072: 0.15 against 0.30).
+bool staged_attn_auto(int dtype, int64_t B, int64_t T, int HQ, int DQ, int DV, bool split);
 // Compute units of the current device (cached per thread), 0 if unknown.
 int device_cus();
 // Its score copies address one batch element's [T, ld] rows with 32-bit
 // buffer offsets.
 constexpr int64_t kStagedMaxScoreBytes = int64_t{1} << 31;
 inline bool staged_attn_fits(int64_t T, int64_t ld) { return T * ld * 4 < kStagedMaxScoreBytes; }
+// Work items (64-query tile, key chunk) of one batch element, passed in the
+// kernel arguments.
+constexpr int kStagedMaxItems = 896;
+// How the staged kernel assigns its blocks.  kStagedPairs: each block takes
+// the 32-query tiles p and ntile-1-p and streams their causal keys.
+// kStagedGroups: each block takes a 64-query group (queries 64m ..
+// 64m+63) and streams its causal keys.  kStagedSplit: each block takes a
+// 64-query group and a chunk of at most CK of its causal keys; groups
+// q_split .. q_split + nsplit - 1 are split, into at most ncmax chunks, and
+// their partial sums take ws_bytes of workspace (part_bytes of rows, then
+// the per-head running max and sum).  The first two use no workspace.
+enum { kStagedPairs = 0, kStagedGroups = 1, kStagedSplit = 2 };
+struct StagedPlan {
+  int mode;
+  int CK;
+  int q_split;
+  int nsplit;
+  int ncmax;
+  int64_t part_bytes;
+  int64_t ws_bytes;
+};
+StagedPlan staged_attn_plan(int64_t B, int64_t T, int HQ, int DQ, bool split);
 hipError_t launch_staged_attn(const float* scores, int64_t ld, const float* thr, const void* Q,
                               const void* K, const void* V, int dtype, int64_t B, int64_t T,
-                              int HQ, int DQ, float scale, float* out, hipStream_t stream);
+                              int HQ, int DQ, float scale, float* out, void* ws, int64_t ws_bytes,
+                              hipStream_t stream);
 
 // Fused forward for T <= kFusedMaxT.
 constexpr int64_t kFusedMaxT = 2048;

@@ -154,8 +154,8 @@ bool sparse_attn_uses_tiles(int dtype, int64_t T, int HQ, int DQ, int DV) {
 
 hipError_t launch_sparse_attn(const float* scores, int64_t ld, const float* thr, const void* Q,
                               const void* K, const void* V, int dtype, int64_t B, int64_t T,
-                              int HQ, int DQ, int DV, float scale, float* out,
-                              hipStream_t stream) {
+                              int HQ, int DQ, int DV, float scale, float* out, void* ws,
+                              int64_t ws_bytes, hipStream_t stream) {
   if (B == 0 || T == 0) return hipSuccess;
   // Dense-masked tiles for long rows, and for rows whose gathers would need
   // head chunks (each chunk re-reads the score row and the list).
@@ -164,10 +164,24 @@ hipError_t launch_sparse_attn(const float* scores, int64_t ld, const float* thr,
     return launch_tile_attn(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, scale, out, stream);
   // Long rows whose K/V rows a wave holds in one slice: each block streams
   // its causal keys once through LDS instead of gathering per query.
-  if (staged_attn_auto(dtype, B, T, HQ, DQ, DV) && staged_attn_fits(T, ld))
-    return launch_staged_attn(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, scale, out, stream);
+  const int64_t need = sparse_attn_workspace_bytes(false, dtype, B, T, HQ, DQ, DV, ld);
+  const bool split = need > 0 && ws != nullptr && ws_bytes >= need &&
+                     (reinterpret_cast<uintptr_t>(ws) & 15u) == 0;
+  if (staged_attn_auto(dtype, B, T, HQ, DQ, DV, split) && staged_attn_fits(T, ld))
+    return launch_staged_attn(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, scale, out, ws,
+                              ws_bytes, stream);
   return launch_sparse_attn_gather(scores, ld, thr, Q, K, V, dtype, B, T, HQ, DQ, DV, scale,
                                    out, stream);
+}
+
+int64_t sparse_attn_workspace_bytes(bool staged, int dtype, int64_t B, int64_t T, int HQ, int DQ,
+                                    int DV, int64_t ld) {
+  if (B <= 0 || T <= 0 || !staged_attn_supported(dtype, HQ, DQ, DV) || !staged_attn_fits(T, ld))
+    return 0;
+  if (!staged && (sparse_attn_uses_tiles(dtype, T, HQ, DQ, DV) ||
+                  !staged_attn_auto(dtype, B, T, HQ, DQ, DV, true)))
+    return 0;
+  return staged_attn_plan(B, T, HQ, DQ, true).ws_bytes;
 }
 
 hipError_t launch_sparse_attn_gather(const float* scores, int64_t ld, const float* thr,

@@ -8,29 +8,35 @@
 // a long row selects a few hundred keys (config 3: k = 256 of up to 4096),
 // the per-query gather pulls each query's K/V rows from L2/MALL on its own
 // (16.6 GB per forward at config 3) although the selected sets of nearby
-// queries are spread over the same key range.  Here a block streams its
-// causal key range once, in tiles of 16 keys copied HBM/L2 -> LDS by the DMA
-// path (buffer_load ... lds through range-checked buffer resources whose
-// base moves with the tile, so a copy costs no per-lane address arithmetic;
-// a ring of 4 slots, 3 tiles ahead, for rows of 1 KiB, and of 2 slots, 1
-// tile ahead, for rows of 2 KiB), and every wave computes its queries'
-// selected pairs of the tile from LDS.
+// queries are spread over the same key range.  Here a block of 16 waves
+// takes 64 queries and streams their causal key range once, in tiles of 16
+// keys copied HBM/L2 -> LDS by the DMA path (buffer_load ... lds through
+// range-checked buffer resources whose base moves with the tile, so a copy
+// costs no per-lane address arithmetic; a ring of 4 slots, 3 tiles ahead,
+// for rows of 1 KiB, and of 2 slots, 1 tile ahead, for rows of 2 KiB), and
+// every wave computes its queries' selected pairs of the tile from LDS.  Per
+// key tile a wave reads its 4 queries' scores (one per lane, copied with
+// the tile), turns them into a 64-bit selection mask, and walks the keys any
+// of its queries selected: it reads the key's K and V slices from LDS once
+// and updates each selecting query.
 //
-// Block = 16 waves = two 32-query tiles of one batch element, tile p and
-// tile ntile-1-p, so every block has about the same causal work (T keys x 32
-// queries) and the short tile's keys come with the long tile's stream.  Wave
-// w owns queries 2w, 2w+1 of each tile.  Per key tile a wave reads its 4
-// queries' scores (one per lane, copied with the tile), turns them into a
-// 64-bit selection mask, and walks the keys any of its queries selected: it
-// reads the key's K and V slices from LDS once and updates each selecting
-// query.
+// Which 64 queries, and which of their keys, a block takes (staged_attn_plan):
+// two 32-query tiles p and ntile-1-p (equal causal work per block), one
+// 64-query group, or a chunk of a 64-query group's keys when the batch has
+// fewer groups than the GPU has compute units -- the chunks' partial softmax
+// sums go to a caller-provided workspace and staged_merge_kernel combines
+// them.  What bounds a block (per-block clock traces at config 3): about 25
+// VALU instructions per selected (query, key) pair, so that a group near
+// the start of the row, whose queries select most of their few keys, takes
+// ~200 us for its ~16k pairs; and, on sparse stretches, the copy of each
+// 64 KiB key tile (issued one tile ahead), ~1.8 us per tile.  A tile pair
+// gives every block the same pair count; the groups stream fewer keys in
+// all; the split spreads the long streams when there are not enough blocks.
 //
-// Measured at config 3 (B=4, T=4096, k=256, HQ=8, D=64, fp32): 0.438 ms
-// against 0.69-0.75 ms for per-query gathers (8-key tiles in a ring of 4:
-// 0.497 ms; with per-lane address arithmetic for the copies: 0.544 ms).
-// What limits it: the barrier per key tile waits for the busiest wave (the
-// selected pairs per wave and tile vary about 1.7x around their mean for
-// 8-key tiles); 16-key tiles average the variation over twice the pairs.
+// Measured at config 3 (B=4, T=4096, k=256, HQ=8, D=64, fp32): 0.434-0.44 ms
+// as tile pairs against 0.69-0.75 ms for per-query gathers (as groups 0.47,
+// split 0.44-0.50); B=8 0.73 ms as groups (0.85 as pairs); B=2 0.24 ms
+// split (0.41 as pairs, 0.37 gathers); B=1 0.18 ms split (0.20 gathers).
 // The threshold entry point takes this kernel only where it measured faster
 // than the gathers (staged_attn_auto).
 //
@@ -40,7 +46,9 @@
 // running max moves only when a logit exceeds it by more than 8 (a factor
 // 2^8), so the accumulator is rescaled on a few keys per query.  Rows that select
 // nothing output NaN (0/0), as the reference.
+#include <algorithm>
 #include <type_traits>
+#include <vector>
 
 #include "dsa_device.h"
 #include "dsa_launch.h"
@@ -49,6 +57,9 @@ namespace dsa {
 namespace {
 
 constexpr int kSTQ = 32;     // queries per tile; a block holds two tiles
+constexpr int kSQ = 2 * kSTQ;  // queries per block (a 64-query group when split)
+constexpr int kSTW = 16;     // waves per block
+constexpr int kSQPW = kSQ / kSTW;
 
 #define DSA_LDS __attribute__((address_space(3)))
 
@@ -64,8 +75,17 @@ struct StagedArgs {
   int DQ;          // head dim (DQ = DV); a row holds 64*E / DQ heads
   float scale_log2;
   float* out;
-  int ntile;       // ceil(T / kSTQ)
+  int CK;          // keys per chunk: a group with more causal keys is split
+  int q_split;     // first 64-query group with more than CK causal keys
+  int nsplit;      // groups q_split .. nq-1 per batch element
+  int ncmax;       // chunks of the longest group
+  float* part;     // split groups' partial sums [B][nsplit][ncmax][kSQ][row]
+  float* part_ml;  // and their (running max + 8, sum) [B][nsplit][ncmax][kSQ][heads][2]
+  // Per batch element, in launch order: tile a | tile b << 12 | chunk << 24
+  // (32-query tiles a <= b; a == b: one tile).
+  uint32_t items[kStagedMaxItems];
 };
+static_assert(sizeof(StagedArgs) <= 4096, "kernel arguments are limited to 4 KiB");
 
 template <typename Tag, int E>
 constexpr int row_bytes() { return kWave * E * Tag::kBytes; }
@@ -149,27 +169,37 @@ __device__ __forceinline__ void lds_slice(const DSA_LDS uint8_t* row, int lane, 
 }
 
 // LPH: lanes per head (DQ / E), a compile-time constant so that the head
-// butterfly is straight-line code.  QPW: queries per wave (QPW/2 from each
-// tile); the block has 64/QPW waves.
+// butterfly is straight-line code.
+//
+// Block blockIdx.x serves batch element blockIdx.x % B and work item
+// items[blockIdx.x / B]: two 32-query tiles a <= b and chunk c of their
+// causal keys, keys [c*CK, min(L, (c+1)*CK)) with L = min(T, 32(b+1)).  Wave
+// w owns queries 2w, 2w+1 of each tile.  The host forms the items one of two
+// ways (staged_attn_plan): tiles p and ntile-1-p in one chunk (every block
+// has about the same causal work, T keys x 32 queries, and the short tile's
+// keys come with the long tile's stream), or tiles 2m, 2m+1 -- the 64-query
+// group m -- with the group's causal keys split into chunks of CK when it
+// has more; the chunks of a split group write partial sums that
+// staged_merge_kernel combines.
 //
 // Pipeline: NS LDS slots (ring_slots), each holding one key tile's K rows,
 // V rows and the block's scores for it, all copied by DMA.  Iteration kt
 // waits for tile kt's copies, passes one barrier (every wave is then done
 // with tile kt-1, whose slot is free), issues the copies of tile kt+NS-1
 // into that slot and computes tile kt.  Every iteration issues the same
-// copies (tiles past the end read as zeros into a slot nobody reads), so the
-// wait is one fixed vmcnt: all but the copies of the NS-2 tiles issued after
-// tile kt's.  The slots are separate LDS objects and the loop is unrolled
-// over them, so the compiler sees that a copy into one slot does not alias
-// reads of another and leaves the copies in flight.
-template <typename Tag, int E, int LPH, int QPW>
-__global__ __launch_bounds__(64 / QPW * kWave) void staged_attn_kernel(StagedArgs a) {
-  static_assert(QPW == 4 || QPW == 8, "4 or 8 queries per wave");
-  constexpr int NW = 64 / QPW;           // waves per block
+// copies (tiles past the chunk read rows that nobody uses, or zeros past
+// row T, into a slot nobody reads), so the wait is one fixed vmcnt: all but
+// the copies of the NS-2 tiles issued after tile kt's.  The slots are
+// separate LDS objects and the loop is unrolled over them, so the compiler
+// sees that a copy into one slot does not alias reads of another and leaves
+// the copies in flight.
+template <typename Tag, int E, int LPH>
+__global__ __launch_bounds__(kSTW * kWave) void staged_attn_kernel(StagedArgs a) {
+  constexpr int QPW = kSQPW;
+  constexpr int NW = kSTW;               // waves per block
   constexpr int NT = NW * kWave;         // threads per block
-  constexpr int HALF = QPW / 2;          // queries per wave from each tile
   constexpr int KT = tile_keys<Tag, E>();
-  static_assert(KT == 8 || KT == 16, "8 or 16 keys per tile");
+  static_assert(KT == 16, "16 keys per tile");
   static_assert(QPW * KT <= kWave, "one score per lane per tile");
   constexpr int SK = slot_bytes<Tag, E>();
   constexpr int NS = ring_slots<Tag, E>();
@@ -180,6 +210,7 @@ __global__ __launch_bounds__(64 / QPW * kWave) void staged_attn_kernel(StagedArg
   using raw = typename Tag::raw;
   constexpr int RB = row_bytes<Tag, E>();
   constexpr int RE = kWave * E;  // elements per K/V row
+  constexpr int HQ = kWave / LPH;  // heads per row
   constexpr int SCB = NW * kWave * 4;  // score bytes per tile (one float per lane)
   // One LDS object per slot (K rows, V rows, scores): separate objects keep
   // the compiler's tracking of copies in flight exact.  With a ring of 2,
@@ -202,23 +233,31 @@ __global__ __launch_bounds__(64 / QPW * kWave) void staged_attn_kernel(StagedArg
   const int lane = lane_id();
   const int T = a.T;
   const int64_t b = static_cast<int64_t>(blockIdx.x) % a.B;
-  const int p = static_cast<int>(static_cast<int64_t>(blockIdx.x) / a.B);
-  const int ta = p, tb = a.ntile - 1 - p;  // ta <= tb
+  const uint32_t item = a.items[static_cast<int64_t>(blockIdx.x) / a.B];
+  const int ta = static_cast<int>(item & 0xfffu);
+  const int tb = static_cast<int>((item >> 12) & 0xfffu);
+  const int chunk = static_cast<int>(item >> 24);
+  const int L = min(T, kSTQ * (tb + 1));  // causal keys of the block's last query
+  const int k0 = chunk * a.CK;
+  const int k1 = min(L, k0 + a.CK);
+  const bool split = L > a.CK;  // only for 64-query groups (ta = 2m, tb = 2m+1)
+  const int nkt = (k1 - k0 + KT - 1) / KT;
+  constexpr int HALF = QPW / 2;  // queries per wave from each tile
 
-  // Query i of this wave: HALF*wave + i % HALF of tile ta (i < HALF) or of
-  // tile tb (unless the pair is one tile).
+  // Query i of this wave: 2*wave + i % 2 of tile ta (i < 2) or of tile tb;
+  // its row in a 64-query group's partial sums is (i < 2 ? 0 : 32) + 2*wave
+  // + i % 2.
   auto query_of = [&](int i) { return (i < HALF ? ta : tb) * kSTQ + HALF * wave + (i % HALF); };
   auto valid = [&](int i, int t) { return t < T && (i < HALF || tb != ta); };
-  const int s_end = min(T, (tb + 1) * kSTQ);  // keys any query of the block reaches
-  const int nkt = (s_end + KT - 1) / KT;
 
-  // This lane's score per key tile: query lane / KT of the wave (lanes past
-  // the wave's QPW queries load a clamped entry and select nothing), key
-  // s0 + lane % KT, clamped into the row (the mask tests causality).
+  // This lane's score per key tile: query lane / KT of the wave, key
+  // s0 + lane % KT, clamped into the row (the mask tests causality).  Keys
+  // at or past k1 are never causal: k1 is L (past every query of the tile)
+  // or a chunk end, where the tile loop stops.
   const int j_l = lane % KT;
   const int i_l = lane / KT;
   const int t_l = (i_l < HALF ? ta : tb) * kSTQ + HALF * wave + (i_l % HALF);
-  const bool v_l = i_l < QPW && t_l < T && (i_l < HALF || tb != ta);
+  const bool v_l = t_l < T && (i_l < HALF || tb != ta);
   const int tc_l = min(t_l, T - 1);
   const float thr_l = a.thr[b * T + tc_l];
   // key s0 + j_l is causal for this lane's query iff s0 <= lim_l (never for
@@ -243,7 +282,7 @@ __global__ __launch_bounds__(64 / QPW * kWave) void staged_attn_kernel(StagedArg
   const int sc_elems = T * static_cast<int>(a.ld);  // < 2^29
   auto copy_tile = [&](auto slot_c, int t) __attribute__((always_inline)) {
     constexpr int S = decltype(slot_c)::value;
-    const int s0 = t * KT;
+    const int s0 = k0 + t * KT;
     const __amdgpu_buffer_rsrc_t rk = span_rsrc(Kb, s0, T, RB);
     const __amdgpu_buffer_rsrc_t rv = span_rsrc(Vb, s0, T, RB);
 #pragma unroll
@@ -280,7 +319,8 @@ __global__ __launch_bounds__(64 / QPW * kWave) void staged_attn_kernel(StagedArg
 
   // mp = running max + 8: a logit moves it only when it exceeds mp, and the
   // weights exp2(x - mp) are the usual exp2(x - max) times 2^-8, a factor
-  // that cancels in acc / l.
+  // that cancels in acc / l (and in the merge of split tiles, which rescales
+  // every chunk to the largest mp).
   float acc[QPW][E];
   float mp[QPW], l[QPW];
 #pragma unroll
@@ -316,15 +356,13 @@ __global__ __launch_bounds__(64 / QPW * kWave) void staged_attn_kernel(StagedArg
     __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(WAITN) : "memory");
     __builtin_amdgcn_s_barrier();
     __asm__ volatile("" ::: "memory");
-    const int s0 = kt * KT;
+    const int s0 = k0 + kt * KT;
     const float sc = *reinterpret_cast<const DSA_LDS float*>(cs[S] + wave * (kWave * 4) + lane * 4);
     // bit i*KT + j: query i of the wave selects key s0 + j (NaN scores and
     // thresholds select nothing)
     const uint64_t sel = ballot((s0 <= lim_l) & (sc >= thr_l));
     copy_tile(std::integral_constant<int, (S + NS - 1) % NS>{}, kt + NS - 1);
-    uint32_t u;
-    if constexpr (KT == 16) u = static_cast<uint32_t>((sel | (sel >> 16) | (sel >> 32) | (sel >> 48)) & 0xffffu);
-    else u = static_cast<uint32_t>((sel | (sel >> 8) | (sel >> 16) | (sel >> 24)) & 0xffu);
+    uint32_t u = static_cast<uint32_t>((sel | (sel >> 16) | (sel >> 32) | (sel >> 48)) & 0xffffu);
     const DSA_LDS uint8_t* kl = ks[S];
     const DSA_LDS uint8_t* vl = vs[S];
     auto process = [&](int j, const float (&kv)[E], const float (&vv)[E]) {
@@ -386,7 +424,7 @@ __global__ __launch_bounds__(64 / QPW * kWave) void staged_attn_kernel(StagedArg
       }
     }
   };
-  // Four tiles per trip: one per slot.
+  // NS tiles per trip: one per slot.
   for (int kt = 0; kt < nkt; kt += NS) {
     tile(S0{}, kt);
     if (kt + 1 >= nkt) break;
@@ -401,10 +439,14 @@ __global__ __launch_bounds__(64 / QPW * kWave) void staged_attn_kernel(StagedArg
   // the copies issued past the end must land before the block exits
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+  // Slot of this chunk's partial rows (split groups only).
+  const int64_t pslot =
+      ((b * a.nsplit + (ta / 2 - a.q_split)) * a.ncmax + chunk) * static_cast<int64_t>(kSQ);
 #pragma unroll
   for (int i = 0; i < QPW; ++i) {
     const int t = query_of(i);
-    if (valid(i, t)) {
+    if (!valid(i, t)) continue;
+    if (!split) {
       const float inv = 1.f / l[i];  // l == 0 only if nothing passed: NaN, as the reference
       float* orow = a.out + (b * T + t) * static_cast<int64_t>(RE) + lane * E;
 #pragma unroll
@@ -412,26 +454,178 @@ __global__ __launch_bounds__(64 / QPW * kWave) void staged_attn_kernel(StagedArg
         *reinterpret_cast<float4*>(orow + e) =
             make_float4(acc[i][e] * inv, acc[i][e + 1] * inv, acc[i][e + 2] * inv,
                         acc[i][e + 3] * inv);
+    } else {
+      const int64_t r = pslot + (i < HALF ? 0 : kSTQ) + HALF * wave + (i % HALF);
+      float* prow = a.part + r * RE + lane * E;
+#pragma unroll
+      for (int e = 0; e < E; e += 4)
+        *reinterpret_cast<float4*>(prow + e) =
+            make_float4(acc[i][e], acc[i][e + 1], acc[i][e + 2], acc[i][e + 3]);
+      if (lane % LPH == 0)  // every lane of a head holds the head's mp and l
+        *reinterpret_cast<float2*>(a.part_ml + (r * HQ + lane / LPH) * 2) = make_float2(mp[i], l[i]);
     }
   }
 }
 
-// Queries per wave by instance (4: 16 waves per block, 4 per SIMD; 8
-// queries per wave and 2 waves per SIMD hid less latency).
-template <typename Tag, int E>
-constexpr int staged_qpw() { return 4; }
+// Output rows of the split tiles from their chunks' partial sums: one wave
+// per query.  With M the largest mp of a head over the chunks, the head's
+// output is sum_c 2^(mp_c - M) acc_c / sum_c 2^(mp_c - M) l_c (a chunk that
+// selected nothing has mp = -inf, l = 0, acc = 0 and weight 0; a row whose
+// chunks all selected nothing comes out 0/0 = NaN, as the reference).
+struct MergeArgs {
+  int64_t B;
+  int T;
+  int CK;
+  int q_split;
+  int nsplit;
+  int ncmax;
+  const float* part;
+  const float* part_ml;
+  float* out;
+};
+
+template <int E, int LPH>
+__global__ __launch_bounds__(256) void staged_merge_kernel(MergeArgs a) {
+  constexpr int RE = kWave * E;
+  constexpr int HQ = kWave / LPH;
+  const int lane = lane_id();
+  const int64_t gq = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);  // split query
+  const int64_t per_b = static_cast<int64_t>(a.nsplit) * kSQ;
+  if (gq >= a.B * per_b) return;
+  const int64_t b = gq / per_b;
+  const int si = static_cast<int>((gq % per_b) / kSQ);
+  const int iq = static_cast<int>(gq % kSQ);
+  const int qt = a.q_split + si;
+  const int t = qt * kSQ + iq;
+  if (t >= a.T) return;
+  const int L = min(a.T, kSQ * (qt + 1));
+  const int nc = (L + a.CK - 1) / a.CK;
+  const int h = lane / LPH;
+  const int64_t r0 = ((b * a.nsplit + si) * a.ncmax) * static_cast<int64_t>(kSQ) + iq;
+  float M = -__builtin_huge_valf();
+  for (int c = 0; c < nc; ++c) M = fmaxf(M, a.part_ml[((r0 + c * kSQ) * HQ + h) * 2]);
+  float acc[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) acc[e] = 0.f;
+  float lsum = 0.f;
+  for (int c = 0; c < nc; ++c) {
+    const int64_t r = r0 + c * kSQ;
+    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (r * HQ + h) * 2);
+    const float w = ml.x == -__builtin_huge_valf() ? 0.f : exp2f(ml.x - M);
+    lsum = fmaf(w, ml.y, lsum);
+    const float* prow = a.part + r * RE + lane * E;
+#pragma unroll
+    for (int e = 0; e < E; e += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(prow + e);
+      acc[e] = fmaf(w, v.x, acc[e]);
+      acc[e + 1] = fmaf(w, v.y, acc[e + 1]);
+      acc[e + 2] = fmaf(w, v.z, acc[e + 2]);
+      acc[e + 3] = fmaf(w, v.w, acc[e + 3]);
+    }
+  }
+  const float inv = 1.f / lsum;
+  float* orow = a.out + (b * a.T + t) * static_cast<int64_t>(RE) + lane * E;
+#pragma unroll
+  for (int e = 0; e < E; e += 4)
+    *reinterpret_cast<float4*>(orow + e) =
+        make_float4(acc[e] * inv, acc[e + 1] * inv, acc[e + 2] * inv, acc[e + 3] * inv);
+}
 
 template <typename Tag, int E, int LPH>
-hipError_t launch(const StagedArgs& a, hipStream_t stream) {
-  constexpr int QPW = staged_qpw<Tag, E>();
-  constexpr int NT = 64 / QPW * kWave;
-  const int64_t npair = (a.ntile + 1) / 2;
-  hipLaunchKernelGGL((staged_attn_kernel<Tag, E, LPH, QPW>), dim3(static_cast<unsigned>(a.B * npair)),
-                     dim3(NT), 0, stream, a);
+hipError_t launch(const StagedArgs& a, int nitems, hipStream_t stream) {
+  hipLaunchKernelGGL((staged_attn_kernel<Tag, E, LPH>),
+                     dim3(static_cast<unsigned>(a.B * nitems)), dim3(kSTW * kWave), 0, stream, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.nsplit == 0) return e;
+  MergeArgs m{a.B, a.T, a.CK, a.q_split, a.nsplit, a.ncmax, a.part, a.part_ml, a.out};
+  const int64_t nq = a.B * a.nsplit * kSQ;
+  hipLaunchKernelGGL((staged_merge_kernel<E, LPH>), dim3(static_cast<unsigned>((nq + 3) / 4)),
+                     dim3(256), 0, stream, m);
   return hipGetLastError();
 }
 
+// The work items of one batch element (encoded as StagedArgs::items), in
+// launch order.  kStagedPairs: tiles p and ntile-1-p, one chunk, p
+// ascending (the longest streams first).  kStagedGroups: the 64-query
+// groups, one chunk each, the last (longest) first.  kStagedSplit: the
+// groups with their causal keys in chunks of CK, the group nearest the
+// start first, then the longest chunk: a query selects a larger share of
+// its keys the fewer it has, so the early groups compute the most pairs per
+// streamed key; they start first, and the short chunks fill the compute
+// units that finish early.  Returns the count, -1 past kStagedMaxItems.
+int staged_items(int64_t T, int mode, int CK, uint32_t* items) {
+  const int ntile = static_cast<int>((T + kSTQ - 1) / kSTQ);
+  auto code = [](int ta, int tb, int c) {
+    return static_cast<uint32_t>(ta) | (static_cast<uint32_t>(tb) << 12) |
+           (static_cast<uint32_t>(c) << 24);
+  };
+  const int nq = (ntile + 1) / 2;
+  if (mode == kStagedPairs || mode == kStagedGroups) {
+    if (nq > kStagedMaxItems) return -1;
+    for (int q = 0; q < nq; ++q) {
+      const int m = nq - 1 - q;
+      items[q] = mode == kStagedPairs ? code(q, ntile - 1 - q, 0)
+                                      : code(2 * m, std::min(2 * m + 1, ntile - 1), 0);
+    }
+    return nq;
+  }
+  struct It { int m, len, c; };
+  std::vector<It> v;
+  for (int m = 0; m < nq; ++m) {
+    const int L = static_cast<int>(std::min<int64_t>(T, int64_t{kSQ} * (m + 1)));
+    for (int c = 0; c * CK < L; ++c) v.push_back({m, std::min(L, (c + 1) * CK) - c * CK, c});
+  }
+  if (static_cast<int>(v.size()) > kStagedMaxItems || (v.empty() ? 0 : v.back().c) > 255) return -1;
+  std::stable_sort(v.begin(), v.end(), [](const It& x, const It& y) {
+    if (x.m != y.m) return x.m < y.m;
+    if (x.len != y.len) return x.len > y.len;
+    return x.c < y.c;
+  });
+  for (size_t i = 0; i < v.size(); ++i)
+    items[i] = code(2 * v[i].m, std::min(2 * v[i].m + 1, ntile - 1), v[i].c);
+  return static_cast<int>(v.size());
+}
+
 }  // namespace
+
+StagedPlan staged_attn_plan(int64_t B, int64_t T, int HQ, int DQ, bool split) {
+  StagedPlan p{};
+  const int64_t nq = (T + kSQ - 1) / kSQ;  // 64-query groups
+  const int cus = std::max(device_cus(), 1);
+  p.CK = 1 << 30;
+  // Measured at T = 4096, HQ = 8, D = 64, k = 256 fp32 on MI355X (256 CUs):
+  // B = 8 0.73 ms as groups against 0.85 as tile pairs; B = 4 0.44 as tile
+  // pairs against 0.44-0.47 as groups, split or not; B = 2 0.238 ms split
+  // into chunks of 512 keys (0.248 with 256, 0.41 as tile pairs); B = 1
+  // 0.176 ms with chunks of 256 (0.216 with 512, 0.41 as tile pairs).
+  if (B * nq >= 2 * cus) {
+    p.mode = kStagedGroups;
+  } else if (B * nq >= cus || !split) {
+    p.mode = kStagedPairs;
+  } else {
+    // Chunks of half the mean number of keys a unit streams, in multiples
+    // of 256.
+    int64_t keys = 0;
+    for (int64_t m = 0; m < nq; ++m) keys += std::min(T, kSQ * (m + 1));
+    int64_t ck = std::max<int64_t>(256, B * keys / cus / 2 / 256 * 256);
+    uint32_t tmp[kStagedMaxItems];
+    while (ck < T && staged_items(T, kStagedSplit, static_cast<int>(ck), tmp) < 0) ck *= 2;
+    if (ck < T) {
+      p.mode = kStagedSplit;
+      p.CK = static_cast<int>(ck);
+    } else {
+      p.mode = kStagedPairs;
+    }
+  }
+  if (p.mode != kStagedSplit) return p;  // no group is split: no workspace
+  p.q_split = p.CK / kSQ;  // groups m >= CK/64 have more than CK causal keys
+  p.nsplit = static_cast<int>(nq - p.q_split);
+  p.ncmax = static_cast<int>((T + p.CK - 1) / p.CK);
+  const int64_t rows = B * p.nsplit * p.ncmax * kSQ;
+  p.part_bytes = rows * HQ * DQ * 4;
+  p.ws_bytes = p.part_bytes + rows * HQ * 2 * 4;
+  return p;
+}
 
 bool staged_attn_supported(int dtype, int HQ, int DQ, int DV) {
   if (DQ != DV || HQ < 1 || DQ < 1) return false;
@@ -444,31 +638,45 @@ bool staged_attn_supported(int dtype, int HQ, int DQ, int DV) {
   return false;
 }
 
-bool staged_attn_auto(int dtype, int64_t B, int64_t T, int HQ, int DQ, int DV) {
+bool staged_attn_auto(int dtype, int64_t B, int64_t T, int HQ, int DQ, int DV, bool split) {
   if (dtype != 0 || T < kStagedMinT || !staged_attn_supported(dtype, HQ, DQ, DV)) return false;
   if (static_cast<int64_t>(HQ) * DQ != 8 * kWave) return false;  // E = 8
+  if (split) return true;
   const int64_t blocks = B * (((T + kSTQ - 1) / kSTQ + 1) / 2);
   return 2 * blocks >= device_cus();
 }
 
 hipError_t launch_staged_attn(const float* scores, int64_t ld, const float* thr, const void* Q,
                               const void* K, const void* V, int dtype, int64_t B, int64_t T,
-                              int HQ, int DQ, float scale, float* out, hipStream_t stream) {
+                              int HQ, int DQ, float scale, float* out, void* ws, int64_t ws_bytes,
+                              hipStream_t stream) {
   if (B == 0 || T == 0) return hipSuccess;
   if (!staged_attn_fits(T, ld)) return hipErrorInvalidValue;
-  StagedArgs a{scores, ld, thr, Q, K, V, B, static_cast<int>(T), DQ,
-               scale * 1.4426950408889634f, out, static_cast<int>((T + kSTQ - 1) / kSTQ)};
+  StagedPlan p = staged_attn_plan(B, T, HQ, DQ, true);
+  if (p.mode == kStagedSplit && (ws == nullptr || ws_bytes < p.ws_bytes ||
+                                 (reinterpret_cast<uintptr_t>(ws) & 15u) != 0))
+    p = staged_attn_plan(B, T, HQ, DQ, false);
+  StagedArgs a{};
+  a.scores = scores; a.ld = ld; a.thr = thr; a.Q = Q; a.K = K; a.V = V; a.B = B;
+  a.T = static_cast<int>(T); a.DQ = DQ; a.scale_log2 = scale * 1.4426950408889634f; a.out = out;
+  a.CK = p.CK; a.q_split = p.q_split; a.nsplit = p.nsplit; a.ncmax = p.ncmax;
+  if (p.nsplit > 0) {
+    a.part = static_cast<float*>(ws);
+    a.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes);
+  }
+  const int nitems = staged_items(T, p.mode, p.CK, a.items);
+  if (nitems < 0) return hipErrorInvalidValue;
   const int E = static_cast<int>(static_cast<int64_t>(HQ) * DQ / kWave);
   const int lph = DQ / E;
 #define DSA_STAGED_LPH(Tag, e)                                      \
   switch (lph) {                                                    \
-    case 1: return launch<Tag, e, 1>(a, stream);                    \
-    case 2: return launch<Tag, e, 2>(a, stream);                    \
-    case 4: return launch<Tag, e, 4>(a, stream);                    \
-    case 8: return launch<Tag, e, 8>(a, stream);                    \
-    case 16: return launch<Tag, e, 16>(a, stream);                  \
-    case 32: return launch<Tag, e, 32>(a, stream);                  \
-    case 64: return launch<Tag, e, 64>(a, stream);                  \
+    case 1: return launch<Tag, e, 1>(a, nitems, stream);            \
+    case 2: return launch<Tag, e, 2>(a, nitems, stream);            \
+    case 4: return launch<Tag, e, 4>(a, nitems, stream);            \
+    case 8: return launch<Tag, e, 8>(a, nitems, stream);            \
+    case 16: return launch<Tag, e, 16>(a, nitems, stream);          \
+    case 32: return launch<Tag, e, 32>(a, nitems, stream);          \
+    case 64: return launch<Tag, e, 64>(a, nitems, stream);          \
   }
   if (dtype == 0) {
     if (E == 4) { DSA_STAGED_LPH(F32, 4) }

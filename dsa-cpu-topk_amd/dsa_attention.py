@@ -83,7 +83,9 @@ def sparse_attention_hip(scores: torch.Tensor, threshold: torch.Tensor, Q, K, V,
     The library picks the kernel: per-query gathers; dense-masked MFMA tiles
     for T >= 4096 with 16-bit Q/K/V and DQ = DV in {64, 128}; K/V staged
     through LDS for fp32 rows of HQ*DQ = 512 at T >= 3072 when the batch
-    gives at least half a block (two 32-query tiles) per compute unit.  Where it would
+    gives at least one 64-query tile per compute unit (with a workspace
+    from the caching allocator, so that long key ranges split over several
+    blocks; dsa_sparse_attn_workspace_bytes gives its size).  Where it would
     take the tiles, the selection is first reduced to a bitmask
     (dsa_selection_mask, 1 bit per (query, key) instead of a 4-byte score
     read once per head) and the tile kernel reads that (dsa_sparse_attn_mask):
@@ -104,17 +106,25 @@ def sparse_attention_hip(scores: torch.Tensor, threshold: torch.Tensor, Q, K, V,
         out = torch.empty(B, T, HQ, DV, device=Q.device, dtype=torch.float32)
     if tiled:
         kernel = "tiled"
+    assert kernel in (None, "tiled", "staged", "mask"), f"unknown kernel {kernel!r}"
     if kernel is None and L.lib().dsa_sparse_attn_uses_mask(L.dtype_code(dt), T, HQ, DQ, DV):
         kernel = "mask"
     if kernel == "mask":
         return _sparse_attention_mask(scores, thr, Q, K, V, out)
-    fn = {None: L.lib().dsa_sparse_attn_threshold,
-          "tiled": L.lib().dsa_sparse_attn_threshold_tiled,
-          "staged": L.lib().dsa_sparse_attn_threshold_staged}[kernel]
-    rc = fn(
-        scores.data_ptr(), T, thr.data_ptr(), Q.data_ptr(), K.data_ptr(), V.data_ptr(),
-        L.dtype_code(dt), B, T, HQ, DQ, DV, 1.0 / math.sqrt(DQ), out.data_ptr(),
-        L.stream_ptr(Q.device))
+    args = (scores.data_ptr(), T, thr.data_ptr(), Q.data_ptr(), K.data_ptr(), V.data_ptr(),
+            L.dtype_code(dt), B, T, HQ, DQ, DV, 1.0 / math.sqrt(DQ), out.data_ptr())
+    if kernel == "tiled":
+        rc = L.lib().dsa_sparse_attn_threshold_tiled(*args, L.stream_ptr(Q.device))
+    else:
+        staged = kernel == "staged"
+        with torch.cuda.device(Q.device):
+            nws = L.lib().dsa_sparse_attn_workspace_bytes(int(staged), L.dtype_code(dt), B, T, HQ,
+                                                          DQ, DV, T)
+        ws = torch.empty(max(nws, 0), device=Q.device, dtype=torch.uint8) if nws > 0 else None
+        fn = (L.lib().dsa_sparse_attn_threshold_staged_ws if staged
+              else L.lib().dsa_sparse_attn_threshold_ws)
+        rc = fn(*args, ws.data_ptr() if ws is not None else None, nws if ws is not None else 0,
+                L.stream_ptr(Q.device))
     L.check(rc, "sparse_attention")
     return out
 

@@ -151,7 +151,7 @@ int dsa_topk_threshold(const float* scores, int64_t rows, int64_t n, int64_t ld,
  *   in head chunks;
  *   the tile kernel below for 16-bit DQ = DV in {64,128} at T >= 4096 or on
  *   wide rows; the staged kernel below for fp32 rows of HQ*DQ = 512 at
- *   T >= 3072 when the batch gives at least half a block per compute unit.
+ *   T >= 3072 when B*ceil(T/64) is at least the compute-unit count.
  * Constraints: HQ, DQ, DV powers of two; a single head of at most 64*16
  *   (fp32) or 64*32 (16-bit) elements; T*HQ*max(DQ,DV)*bytes < 4 GiB;
  *   ld >= T.
@@ -160,6 +160,38 @@ int dsa_sparse_attn_threshold(const float* scores, int64_t ld, const float* thr,
                               const void* Q, const void* K, const void* V,
                               int dtype, int64_t B, int64_t T, int HQ, int DQ,
                               int DV, float scale, float* out, void* stream);
+
+/*
+ * dsa_sparse_attn_threshold with a device workspace: where it takes the
+ * staged kernel, that kernel splits the causal keys of its long query tiles
+ * into chunks run by separate blocks (the blocks then stream about the same
+ * number of keys each) and a second launch combines the chunks' partial
+ * softmax sums.  workspace_bytes below what
+ * dsa_sparse_attn_workspace_bytes(0, ...) returns (or a null or
+ * non-16-byte-aligned workspace) runs without the split, as
+ * dsa_sparse_attn_threshold does.  The workspace is device memory of the
+ * stream's device that no other work uses until the launches complete; its
+ * contents on entry do not matter.  Same sel and O (the chunks' sums are
+ * combined in another order: results differ in the last bits).
+ * Replaces: sparse_attention_with_threshold_triton's launch,
+ *           reference dsa_attention.py:234-324 (same contract as above);
+ *           the workspace has no counterpart there.
+ */
+int dsa_sparse_attn_threshold_ws(const float* scores, int64_t ld, const float* thr,
+                                 const void* Q, const void* K, const void* V,
+                                 int dtype, int64_t B, int64_t T, int HQ, int DQ,
+                                 int DV, float scale, float* out, void* workspace,
+                                 int64_t workspace_bytes, void* stream);
+
+/*
+ * Workspace bytes with which dsa_sparse_attn_threshold_ws (staged = 0) or
+ * dsa_sparse_attn_threshold_staged_ws (staged = 1) splits the staged
+ * kernel's long tiles on the current device (the split follows its
+ * compute-unit count); 0 when that call uses no workspace for the shape.
+ * No counterpart in the reference (its Triton launch allocates nothing).
+ */
+int64_t dsa_sparse_attn_workspace_bytes(int staged, int dtype, int64_t B, int64_t T, int HQ,
+                                        int DQ, int DV, int64_t ld);
 
 /*
  * dsa_sparse_attn_threshold computed as dense-masked MFMA tiles: the same
@@ -182,16 +214,18 @@ int dsa_sparse_attn_threshold_tiled(const float* scores, int64_t ld, const float
 
 /*
  * dsa_sparse_attn_threshold with each block's causal K/V rows staged through
- * LDS: a block streams the keys of two 32-query tiles (a long and a short
- * one) once, in tiles of 16 keys copied by DMA, and every wave computes its
+ * LDS: a block takes 64 consecutive queries and streams their causal keys
+ * once, in tiles of 16 keys copied by DMA, and every wave computes its
  * queries' selected pairs from LDS -- nearby queries select over the same
  * key range, so the K/V bytes read from L2/MALL drop by the block's query
- * count compared with per-query gathers.  dsa_sparse_attn_threshold switches
- * to it by itself for fp32 rows of HQ*DQ = 512 at T >= 3072 when
- * B * ceil(ceil(T/32)/2) blocks give at least half a block per compute unit
- * (other shapes measured faster with the gathers); this entry point runs it
- * at any T.  Same sel and O,
- * fp32 arithmetic (the softmax sums in a different order than the gathers).
+ * count compared with per-query gathers.  Blocks run longest first.
+ * dsa_sparse_attn_threshold switches to it by itself for fp32 rows of
+ * HQ*DQ = 512 at T >= 3072 when B*ceil(T/64) is at least the compute-unit
+ * count (other shapes measured faster with the gathers); this entry point
+ * runs it at any T.  Same sel and O, fp32 arithmetic (the softmax sums in a
+ * different order than the gathers).  Without a workspace every block
+ * streams its tile's whole causal range; the _ws form below splits long
+ * ranges.
  * Replaces: _sparse_attn_kernel + sparse_attention_with_threshold_triton,
  *           reference dsa_attention.py:234-324 (same contract as above).
  * Constraints: DQ = DV; HQ*DQ = 256 or 512 (fp32) or 512 (bf16/fp16) with
@@ -203,6 +237,20 @@ int dsa_sparse_attn_threshold_staged(const float* scores, int64_t ld, const floa
                                      const void* Q, const void* K, const void* V,
                                      int dtype, int64_t B, int64_t T, int HQ, int DQ,
                                      int DV, float scale, float* out, void* stream);
+
+/*
+ * dsa_sparse_attn_threshold_staged with the workspace of
+ * dsa_sparse_attn_threshold_ws (size from
+ * dsa_sparse_attn_workspace_bytes(1, ...)): long key ranges are split into
+ * chunks, and a second launch combines them.
+ * Replaces: as dsa_sparse_attn_threshold_staged; the workspace has no
+ *           counterpart in the reference.
+ */
+int dsa_sparse_attn_threshold_staged_ws(const float* scores, int64_t ld, const float* thr,
+                                        const void* Q, const void* K, const void* V,
+                                        int dtype, int64_t B, int64_t T, int HQ, int DQ,
+                                        int DV, float scale, float* out, void* workspace,
+                                        int64_t workspace_bytes, void* stream);
 
 /*
  * Selection bitmask of the threshold selection, for dsa_sparse_attn_mask.

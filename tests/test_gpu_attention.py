@@ -7,6 +7,7 @@ import math
 import pytest
 import torch
 
+import _dsa_lib as L
 from dsa_attention import sparse_attention_hip, sparse_attention_with_threshold_triton
 from helpers import close, say
 from oracle import dsa_oracle as O
@@ -369,8 +370,9 @@ def test_wide_rows_threshold_wrapper(dev, dtype, HQ, DQ, DV, T, k):
 
 
 # ---------------------------------------------------------------------------
-# Staged kernel (K/V streamed through LDS per block of two 32-query tiles),
-# forced at small T; the threshold entry point takes it for T >= 2048.
+# Staged kernel (K/V streamed through LDS per block of 64 consecutive
+# queries), forced at small T; the threshold entry point takes it for fp32
+# rows of 512 at T >= 3072.
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("B,T,HQ,D,k,dtype", [
     (1, 64, 8, 64, 8, torch.float32),       # two tiles, one pair
@@ -430,9 +432,9 @@ def test_staged_and_gather_agree(dev):
 
 def test_staged_auto_at_config3_shape(dev):
     """B = 4, T = 4096 fp32, HQ = 8, D = 64 (config 3's attention): the
-    threshold entry point runs the staged kernel (256 blocks of two 32-query
-    tiles: at least half a block per compute unit); sampled rows against the
-    oracle."""
+    threshold entry point runs the staged kernel (256 tiles of 64 queries, at
+    least one per compute unit; long key ranges split over two blocks);
+    sampled rows against the oracle."""
     from helpers import sample_rows
 
     B, T, HQ, D, k = 4, 4096, 8, 64, 256
@@ -448,6 +450,90 @@ def test_staged_auto_at_config3_shape(dev):
     rows = sample_rows(T, 40, seed=3, include=(0, 1, 255, 256, 4095))
     want = O.sparse_attn_threshold(scores[:, rows], thr[:, rows], Q, K, V, rows=rows)
     ok, err, _ = close(out[:, rows].cpu(), want, 1e-4, 1e-4)
+    assert ok, f"max abs err {err}"
+
+
+def _staged_plain(scores, thr, Q, K, V):
+    """The staged entry point without a workspace (no tile is split)."""
+    B, T, HQ, D = Q.shape
+    dt = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[Q.dtype]
+    out = torch.empty(B, T, HQ, D, device=Q.device, dtype=torch.float32)
+    rc = L.lib().dsa_sparse_attn_threshold_staged(
+        scores.data_ptr(), T, thr.data_ptr(), Q.data_ptr(), K.data_ptr(), V.data_ptr(), dt, B, T,
+        HQ, D, D, 1.0 / math.sqrt(D), out.data_ptr(), L.stream_ptr(Q.device))
+    L.check(rc, "staged")
+    return out
+
+
+@pytest.mark.parametrize("B,T,HQ,D,k,dtype", [
+    (1, 1300, 8, 64, 100, torch.float32),   # ragged T; tiles split into up to 3 chunks
+    (2, 1100, 4, 64, 60, torch.float32),    # E = 4 (rows of 256)
+    (1, 1000, 8, 64, 50, torch.bfloat16),
+])
+def test_staged_split_tiles(dev, B, T, HQ, D, k, dtype):
+    """Shapes where the staged kernel splits long key ranges into chunks (a
+    workspace from dsa_sparse_attn_workspace_bytes) and merges them: against
+    the oracle, and against the same kernel run without the split."""
+    nws = L.lib().dsa_sparse_attn_workspace_bytes(1, {torch.float32: 0, torch.bfloat16: 1}[dtype],
+                                                  B, T, HQ, D, D, T)
+    assert nws > 0, "this shape must split"
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    out = run_case(dev, B, T, HQ, D, D, kth(k), dtype=dtype, rtol=tol, atol=tol, kernel="staged")
+    _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, HQ, D, D, dtype=dtype, seed0=0)
+    g = torch.Generator().manual_seed(17)
+    scores = torch.randn(B, T, T, generator=g)
+    scores = torch.where(torch.rand(B, T, T, generator=g) < 0.1, 0.0, scores)
+    thr = kth(k)(scores)
+    plain = _staged_plain(scores.to(dev), thr.to(dev), Q.to(dev), K.to(dev), V.to(dev))
+    torch.cuda.synchronize()
+    assert float((out - plain).abs().max()) <= 1e-5
+
+
+def test_staged_groups_mode(dev):
+    """B*ceil(T/64) >= 2x the compute units: the staged kernel takes one
+    64-query group per block (no tile pairs, no split).  All rows against
+    the gathers (the threshold entry point's choice below T = 3072), sampled
+    rows against the oracle."""
+    from helpers import sample_rows
+
+    B, T, HQ, D, k = 16, 2048, 8, 64, 100
+    _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, HQ, D, D, seed0=31)
+    scores = torch.randn(B, T, T, generator=torch.Generator().manual_seed(32))
+    thr = kth(k)(scores)
+    sd, td, Qd, Kd, Vd = (x.to(dev) for x in (scores, thr, Q, K, V))
+    st = sparse_attention_hip(sd, td, Qd, Kd, Vd, kernel="staged")
+    ga = sparse_attention_hip(sd, td, Qd, Kd, Vd)
+    torch.cuda.synchronize()
+    assert float((st - ga).abs().max()) <= 1e-5
+    rows = sample_rows(T, 24, seed=5, include=(0, 63, 64, 2047))
+    want = O.sparse_attn_threshold(scores[:3, rows], thr[:3, rows], Q[:3], K[:3], V[:3], rows=rows)
+    ok, err, _ = close(st[:3, rows].cpu(), want, 1e-4, 1e-4)
+    assert ok, f"max abs err {err}"
+
+
+def test_staged_split_chunks_that_select_nothing(dev):
+    """Rows of split tiles whose selection falls in one chunk only (the other
+    chunks' partial sums are empty and weigh nothing), rows that select
+    nothing at all (NaN threshold: NaN through the merge), every causal key
+    (-inf threshold) and large logits."""
+    B, T, HQ, D, k = 1, 1200, 8, 64, 50
+    _, _, _, Q, K, V = O.make_inputs(B, T, 1, 1, HQ, D, D, seed0=21)
+    g = torch.Generator().manual_seed(22)
+    scores = torch.randn(B, T, T, generator=g)
+    scores[0, 1100, :600] = -10.0    # top-k of row 1100 all in keys >= 600
+    scores[0, 1101, 512:] = -10.0    # top-k of row 1101 all in keys < 512
+    scores[0, 1150, :1100] = -10.0   # top-k of row 1150 all in the last keys
+    thr = kth(k)(scores)
+    thr[0, 1000] = math.nan
+    thr[0, 1199] = math.nan
+    thr[0, 900] = -math.inf
+    out = sparse_attention_hip(scores.to(dev), thr.to(dev), (Q * 8).to(dev), (K * 8).to(dev),
+                               V.to(dev), kernel="staged").cpu()
+    assert bool(torch.isnan(out[0, 1000]).all()) and bool(torch.isnan(out[0, 1199]).all())
+    keep = torch.ones(T, dtype=torch.bool)
+    keep[[1000, 1199]] = False
+    want = O.sparse_attn_threshold(scores, thr, Q * 8, K * 8, V)
+    ok, err, _ = close(out[:, keep], want[:, keep], 1e-4, 1e-4)
     assert ok, f"max abs err {err}"
 
 
