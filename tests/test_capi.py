@@ -178,6 +178,41 @@ def test_sparse_attn_rejects_bad_arguments():
     assert call(a7=0)[0] == L.DSA_OK
 
 
+def test_sparse_attn_workspace_entries_check_arguments():
+    """The _ws forms validate like the plain ones, refuse a negative
+    workspace size, and accept none (B = 0: nothing launched)."""
+    for f, staged in ((L.lib().dsa_sparse_attn_threshold_ws, False),
+                      (L.lib().dsa_sparse_attn_threshold_staged_ws, True)):
+        def call(ws=None, nws=0, **kw):
+            a = [FAKE, 4096, FAKE, FAKE, FAKE, FAKE, L.DSA_F32, 2, 4096, 8, 64, 64, 0.125, FAKE,
+                 ws, nws, None]
+            for i, v in kw.items():
+                a[int(i[1:])] = v
+            return _rc(f, *a)
+
+        assert call(a1=32)[0] == L.DSA_EINVAL                # ld < T
+        assert call(a12=float("inf"))[0] == L.DSA_EINVAL     # scale
+        assert call(nws=-1)[0] == L.DSA_EINVAL               # negative workspace size
+        assert call(a7=0)[0] == L.DSA_OK                     # B = 0
+        assert call(a7=0, ws=FAKE, nws=1 << 20)[0] == L.DSA_OK
+        if staged:  # the staged kernel's own shape rule
+            assert call(a9=4, a10=32, a11=32)[0] == L.DSA_EUNSUPPORTED
+
+
+def test_sparse_attn_workspace_bytes_zero_where_unused():
+    """No workspace for shapes the staged kernel does not take (16-bit rows
+    of 512 at T = 4096 go to the tile kernel, rows of 128 to the gathers,
+    T below 3072 stays on the gathers), for bad arguments, and for B = 0."""
+    f = L.lib().dsa_sparse_attn_workspace_bytes
+    assert f(0, L.DSA_BF16, 1, 4096, 8, 64, 64, 4096) == 0
+    assert f(0, L.DSA_F32, 4, 4096, 4, 32, 32, 4096) == 0
+    assert f(0, L.DSA_F32, 1, 2048, 8, 64, 64, 2048) == 0
+    assert f(0, L.DSA_F32, 0, 4096, 8, 64, 64, 4096) == 0
+    assert f(1, L.DSA_F32, 1, 4096, 8, 64, 64, 100) == 0     # ld < T
+    assert f(1, 9, 1, 4096, 8, 64, 64, 4096) == 0            # unknown dtype
+    assert f(1, L.DSA_F32, 1, 4096, 4, 32, 32, 4096) == 0    # not a staged shape
+
+
 def test_sparse_attn_accepts_wide_rows():
     """Rows wider than one wave's registers are accepted (head chunks, or the
     tile kernel for 16-bit D in {64,128}); a single head wider than a wave

@@ -489,6 +489,36 @@ def test_staged_split_tiles(dev, B, T, HQ, D, k, dtype):
     assert float((out - plain).abs().max()) <= 1e-5
 
 
+def test_staged_workspace_too_small_runs_unsplit(dev):
+    """A workspace below dsa_sparse_attn_workspace_bytes (or misaligned)
+    runs the staged kernel without the split: the plain entry point's result,
+    bit for bit; the right size splits (equal within rounding)."""
+    B, T, HQ, D, k = 1, 1300, 8, 64, 100
+    _, _, _, Q, K, V = (x.to(dev) for x in O.make_inputs(B, T, 1, 1, HQ, D, D, seed0=41))
+    scores = torch.randn(B, T, T, generator=torch.Generator().manual_seed(42))
+    thr = kth(k)(scores).to(dev)
+    scores = scores.to(dev)
+    nws = L.lib().dsa_sparse_attn_workspace_bytes(1, 0, B, T, HQ, D, D, T)
+    assert nws > 0
+    ws = torch.empty(nws + 16, device=dev, dtype=torch.uint8)
+    plain = _staged_plain(scores, thr, Q, K, V)
+
+    def run(ptr, n):
+        out = torch.empty(B, T, HQ, D, device=dev)
+        rc = L.lib().dsa_sparse_attn_threshold_staged_ws(
+            scores.data_ptr(), T, thr.data_ptr(), Q.data_ptr(), K.data_ptr(), V.data_ptr(), 0, B,
+            T, HQ, D, D, 1.0 / math.sqrt(D), out.data_ptr(), ptr, n, L.stream_ptr(dev))
+        L.check(rc, "staged_ws")
+        return out
+
+    small = run(ws.data_ptr(), nws - 1)
+    misaligned = run(ws.data_ptr() + 4, nws)
+    split = run(ws.data_ptr(), nws)
+    torch.cuda.synchronize()
+    assert torch.equal(small, plain) and torch.equal(misaligned, plain)
+    assert float((split - plain).abs().max()) <= 1e-5
+
+
 def test_staged_groups_mode(dev):
     """B*ceil(T/64) >= 2x the compute units: the staged kernel takes one
     64-query group per block (no tile pairs, no split).  All rows against
