@@ -181,11 +181,16 @@ __device__ __forceinline__ void indexer_rows(const typename Tag::raw* __restrict
         f32x4 acc[KB];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) acc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // the unit's MFMAs at raised wave priority, its epilogue at the normal
+        // one: the SIMD's other waves' VALU work fills in behind the MFMAs
+        // (fused kernel, config 1: 25.38 -> 25.22 us)
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int i = 0; i < S::kSteps; ++i) {
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) acc[kb] = a.mfma(i, bk[kb], acc[kb]);
         }
+        __builtin_amdgcn_s_setprio(0);
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
