@@ -824,8 +824,11 @@ constexpr int kFinGather = 64;   // kept values of one finishing bin ranked in r
 // every selected entry at #(above before it) + min(#(equal before it), k -
 // #above), ascending positions -- emit_indices' rule without a pass per
 // chunk.  MASK (the same rows): the bitmap's words are the bitmask.
+// Eight blocks per CU (at most 64 VGPRs; the LDS columns allow eight): at
+// config 4 thresholds 101 -> 98 us, with indices 156 -> 152, the bitmask
+// 129 -> 127 against six (the bitmask and index forms spill a few SGPRs).
 template <int NT, bool IDX, bool MASK = false>
-__global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
+__global__ __launch_bounds__(NT, 8) void topk_bracket_kernel(SelectArgs a) {
   // IDX: exactly-k indices; MASK: the selection bitmask (a.mask), both from
   // the row's flag bitmap below.
   static_assert(!(IDX && MASK), "one output mode");
@@ -1107,8 +1110,11 @@ __global__ __launch_bounds__(NT, 6) void topk_bracket_kernel(SelectArgs a) {
     // bitmap; wave 0 then finishes the threshold alone and sets the bits of
     // the kept values at or above it.  (Waves held at a barrier while wave 0
     // finishes cost more streaming throughput than wave 0's longer tail:
-    // config 4, 9 us.)  The s-th kept value of a thread is the s-th set bit
-    // of its kept mask over the sample chunks' nibbles, then over the rest.
+    // config 4, 9 us.  Leaving only each thread's flag words and list range
+    // and having wave 0 expand them into the bitmask was no faster: 130 us
+    // either way, the work moved into the tail.)  The s-th kept value of a
+    // thread is the s-th set bit of its kept mask over the sample chunks'
+    // nibbles, then over the rest.
     uint16_t* posl = reinterpret_cast<uint16_t*>(lds + kIdxMapWord + 16 * NT / 4);
     static_assert(!MASK || kIdxMapWord + 16 * NT / 4 + kCandCap / 2 <= CAP * NT, "the bit list fits");
     if constexpr (MASK) {
