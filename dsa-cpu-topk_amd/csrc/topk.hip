@@ -1123,17 +1123,19 @@ __global__ __launch_bounds__(NT, 8) void topk_bracket_kernel(SelectArgs a) {
       uint64_t smask = 0;
 #pragma unroll
       for (int q = 0; q < 4; ++q) smask |= uint64_t{15} << (4 * sample_chunk(q));
-      uint64_t rem = kpt & smask, rest = kpt & ~smask;
-      for (uint32_t i = 0; i < kc; ++i) {
-        if (rem == 0u) {
-          rem = rest;
-          rest = 0u;
+      // Two walks, one per group (a single walk that switches groups when
+      // the first runs out costs 4 us more at config 4).
+      uint16_t* pl = posl + kbase;
+      auto walk = [&](uint64_t m) {
+        while (m != 0u) {
+          const int bp = static_cast<int>(__builtin_ctzll(m));
+          m &= m - 1u;
+          // bit (bp & 3) of byte (bp >> 2) * NT + tid
+          *pl++ = static_cast<uint16_t>(((((bp >> 2) * NT + tid)) << 3) | (bp & 3));
         }
-        const int bp = static_cast<int>(__builtin_ctzll(rem));
-        rem &= rem - 1u;
-        // bit (bp & 3) of byte (bp >> 2) * NT + tid
-        posl[kbase + i] = static_cast<uint16_t>(((((bp >> 2) * NT + tid)) << 3) | (bp & 3));
-      }
+      };
+      walk(kpt & smask);
+      walk(kpt & ~smask);
     }
     block_sync_lds();
     if (MASK && wid != 0) return;
@@ -1148,8 +1150,20 @@ __global__ __launch_bounds__(NT, 8) void topk_bracket_kernel(SelectArgs a) {
     };
     if (wid == 0) {  // one wave finishes on the kept list
       const uint32_t krem = ku - tot_above;
+      // (MASK: four LDS reads in flight per step -- config 4 bitmask 1 us
+      // faster, thresholds and indices 1-2 us slower; the steps are
+      // wave-uniform, so a ballot inside f sees every lane that still has a
+      // value)
       auto visit_kept = [&](auto&& f) {
-        for (uint32_t i = lane; i < ktot; i += kWave) f(__uint_as_float(lds[i]));
+        uint32_t b = 0;
+        for (; MASK && b + 4 * kWave <= ktot; b += 4 * kWave) {
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] = __uint_as_float(lds[b + q * kWave + lane]);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) f(v[q]);
+        }
+        for (uint32_t i = b + lane; i < ktot; i += kWave) f(__uint_as_float(lds[i]));
       };
       // Value bins over the kept values' own range (all below fhi, so NaN is
       // never kept; -inf may be).
@@ -1232,7 +1246,20 @@ __global__ __launch_bounds__(NT, 8) void topk_bracket_kernel(SelectArgs a) {
         // the kept values at or above thr set their bits
         const float thr = res + 0.0f;
         uint32_t* fbw = reinterpret_cast<uint32_t*>(fb);
-        for (uint32_t i = lane; i < ktot; i += kWave) {
+        uint32_t b = 0;
+        for (; b + 4 * kWave <= ktot; b += 4 * kWave) {
+          float v[4];
+          uint32_t p[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            v[q] = __uint_as_float(lds[b + q * kWave + lane]);
+            p[q] = posl[b + q * kWave + lane];
+          }
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (v[q] >= thr) atomicOr(&fbw[p[q] >> 5], 1u << (p[q] & 31u));
+        }
+        for (uint32_t i = b + lane; i < ktot; i += kWave) {
           if (__uint_as_float(lds[i]) >= thr) {
             const uint32_t pb = posl[i];
             atomicOr(&fbw[pb >> 5], 1u << (pb & 31u));
@@ -1245,7 +1272,18 @@ __global__ __launch_bounds__(NT, 8) void topk_bracket_kernel(SelectArgs a) {
 #pragma unroll
         for (int q = 0; q < NW; ++q) {
           const int w = lane + kWave * q;
-          if (w < nw) a.mask[row * a.ldm + w] = nib(reinterpret_cast<const uint4*>(fb)[w], 0);
+          if (w < nw) {
+            // The bytes hold their flags in the low nibble only: one shift
+            // and OR puts two bytes' nibbles side by side, and a byte
+            // permute takes those of four bytes (2 us faster at config 4
+            // than nibble masks and shifts).
+            const uint4 v = reinterpret_cast<const uint4*>(fb)[w];
+            auto pack2 = [](uint32_t lo, uint32_t hi) {
+              return __builtin_amdgcn_perm(hi | (hi >> 4), lo | (lo >> 4), 0x06040200u);
+            };
+            a.mask[row * a.ldm + w] = static_cast<uint64_t>(pack2(v.x, v.y)) |
+                                      (static_cast<uint64_t>(pack2(v.z, v.w)) << 32);
+          }
         }
       }
     }  // wave 0
