@@ -1139,14 +1139,16 @@ __global__ __launch_bounds__(NT, 8) void topk_bracket_kernel(SelectArgs a) {
     }
     block_sync_lds();
     if (MASK && wid != 0) return;
-    // nibble `sh` of each of 16 bytes -> 64 bits (the bitmap's 64 positions)
-    auto nib = [](uint4 v, int sh) {
-      auto w16 = [sh](uint32_t w) {
-        w >>= sh;
-        return (w & 0xfu) | ((w >> 4) & 0xf0u) | ((w >> 8) & 0xf00u) | ((w >> 12) & 0xf000u);
+    // The low nibbles of 16 bytes whose high nibbles are 0 -> 64 bits (the
+    // bitmap's 64 positions, byte i's at bits 4i .. 4i+3): one shift and OR
+    // puts two bytes' nibbles side by side, and a byte permute takes those
+    // of four bytes (config 4: bitmask 2 us faster than a mask and a shift
+    // per nibble, the index form 3-4 us with the walks below).
+    auto pack_nibbles = [](uint4 v) {
+      auto pack2 = [](uint32_t lo, uint32_t hi) {
+        return __builtin_amdgcn_perm(hi | (hi >> 4), lo | (lo >> 4), 0x06040200u);
       };
-      return static_cast<uint64_t>(w16(v.x)) | (static_cast<uint64_t>(w16(v.y)) << 16) |
-             (static_cast<uint64_t>(w16(v.z)) << 32) | (static_cast<uint64_t>(w16(v.w)) << 48);
+      return static_cast<uint64_t>(pack2(v.x, v.y)) | (static_cast<uint64_t>(pack2(v.z, v.w)) << 32);
     };
     if (wid == 0) {  // one wave finishes on the kept list
       const uint32_t krem = ku - tot_above;
@@ -1272,18 +1274,7 @@ __global__ __launch_bounds__(NT, 8) void topk_bracket_kernel(SelectArgs a) {
 #pragma unroll
         for (int q = 0; q < NW; ++q) {
           const int w = lane + kWave * q;
-          if (w < nw) {
-            // The bytes hold their flags in the low nibble only: one shift
-            // and OR puts two bytes' nibbles side by side, and a byte
-            // permute takes those of four bytes (2 us faster at config 4
-            // than nibble masks and shifts).
-            const uint4 v = reinterpret_cast<const uint4*>(fb)[w];
-            auto pack2 = [](uint32_t lo, uint32_t hi) {
-              return __builtin_amdgcn_perm(hi | (hi >> 4), lo | (lo >> 4), 0x06040200u);
-            };
-            a.mask[row * a.ldm + w] = static_cast<uint64_t>(pack2(v.x, v.y)) |
-                                      (static_cast<uint64_t>(pack2(v.z, v.w)) << 32);
-          }
+          if (w < nw) a.mask[row * a.ldm + w] = pack_nibbles(reinterpret_cast<const uint4*>(fb)[w]);
         }
       }
     }  // wave 0
@@ -1296,19 +1287,19 @@ __global__ __launch_bounds__(NT, 8) void topk_bracket_kernel(SelectArgs a) {
       uint64_t smask = 0;
 #pragma unroll
       for (int q = 0; q < 4; ++q) smask |= uint64_t{15} << (4 * sample_chunk(q));
-      uint64_t rem = kpt & smask, rest = kpt & ~smask;
       uint64_t gt = abv, eq = 0;
-      for (uint32_t s = 0; s < kc; ++s) {
-        if (rem == 0u) {
-          rem = rest;
-          rest = 0u;
+      uint32_t s = kbase;
+      auto walk = [&](uint64_t m) {  // one walk per group, as for the bitmask
+        while (m != 0u) {
+          const uint64_t bit = m & (0u - m);
+          m ^= bit;
+          const float v = __uint_as_float(lds[s++]);
+          gt |= v > thr ? bit : 0u;
+          eq |= v == thr ? bit : 0u;
         }
-        const uint64_t bit = rem & (0u - rem);
-        rem ^= bit;
-        const float v = __uint_as_float(lds[kbase + s]);
-        gt |= v > thr ? bit : 0u;
-        eq |= v == thr ? bit : 0u;
-      }
+      };
+      walk(kpt & smask);
+      walk(kpt & ~smask);
 #pragma unroll
       for (int j = 0; j < 16; ++j)
         fb[j * NT + tid] = static_cast<uint8_t>(((gt >> (4 * j)) & 15u) | (((eq >> (4 * j)) & 15u) << 4));
@@ -1317,7 +1308,10 @@ __global__ __launch_bounds__(NT, 8) void topk_bracket_kernel(SelectArgs a) {
       // equal) counts places them, and it walks its set bits only.  The k
       // indices are staged in LDS and written out coalesced.
       const uint4 fv = reinterpret_cast<const uint4*>(fb)[tid];
-      const uint64_t G = nib(fv, 0), Eq = nib(fv, 4);
+      constexpr uint32_t kLo = 0x0f0f0f0fu;  // "above" in the low nibbles, "equal" in the high
+      const uint64_t G = pack_nibbles(make_uint4(fv.x & kLo, fv.y & kLo, fv.z & kLo, fv.w & kLo));
+      const uint64_t Eq = pack_nibbles(make_uint4((fv.x >> 4) & kLo, (fv.y >> 4) & kLo,
+                                                  (fv.z >> 4) & kLo, (fv.w >> 4) & kLo));
       {
         uint32_t tot;
         const uint32_t ex = block_exclusive_sum<NT>(
