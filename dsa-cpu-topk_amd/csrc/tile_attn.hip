@@ -44,8 +44,9 @@
 //                   key tile 2j+1
 //                   -> lane l: query l%16, dims 4(l/16)+r of each 16-dim tile
 // P is rounded to the input's 16-bit type for the second product and for
-// the softmax normaliser, which is one more MFMA per fragment (ones . P^T),
-// so numerator and denominator sum the same probabilities (the reference
+// the softmax normaliser, which sums those 16-bit values with v_dot2 against
+// (1, 1) (fp32 accumulation), so numerator and denominator sum the same
+// probabilities (the reference
 // uses fp32 probabilities; the difference is far inside the 16-bit
 // tolerance); everything else is fp32.  Rows that select nothing get
 // 0/0 = NaN, as the reference.
@@ -109,6 +110,11 @@ struct Mfma16x16x32<BF16> {
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
   static constexpr uint32_t kOnes = 0x3f803f80u;  // two bf16 1.0
+  static __device__ __forceinline__ float dot2_ones(uint32_t w, float acc) {  // acc + w.lo + w.hi
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w),
+                                           __builtin_bit_cast(bf16x2, kOnes), acc, false);
+  }
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) {  // one v_cvt_pk_bf16_f32
     typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
     typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -123,6 +129,11 @@ struct Mfma16x16x32<F16> {
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
   static constexpr uint32_t kOnes = 0x3c003c00u;  // two f16 1.0
+  static __device__ __forceinline__ float dot2_ones(uint32_t w, float acc) {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), __builtin_bit_cast(f16x2, kOnes), acc,
+                                  false);
+  }
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
     typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
     typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -200,8 +211,11 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
   // Bitmask form: the bias of the four keys one nibble of a mask word
   // covers, entry n = {bit r of n set ? 0 : -inf, r = 0..3} (256 bytes).
   // The S accumulators start from it, so an unselected key's logit leaves
-  // the MFMA as -inf + logit and a selected one as +0 + logit.
-  __shared__ __align__(16) float btab[MASK ? 64 : 4];
+  // the MFMA as -inf + logit and a selected one as +0 + logit.  Its larger
+  // alignment puts it at LDS address 0, so an entry's address is the nibble
+  // times 16 with no base to add (one VALU instruction less per nibble;
+  // past the 64 KB of K/V tiles the base does not fit the read's offset).
+  __shared__ __align__(1024) float btab[MASK ? 64 : 4];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS targets in SGPRs
@@ -276,11 +290,13 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
   }
 
   float m[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()};
-  // Softmax normaliser per query as an MFMA accumulator: ones . P^T sums the
-  // tile's (16-bit) probabilities over all 64 keys of the tile, the same
-  // values the O product uses; every register of a query's lanes holds it.
-  f32x4 lacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-  const u32x4 ones = u32x4{M::kOnes, M::kOnes, M::kOnes, M::kOnes};
+  // Softmax normaliser per query: this lane's part, the sum of the 16-bit
+  // probabilities of its 16 keys per tile (the values the O product uses),
+  // two at a time by v_dot2 against (1, 1); the query's four lanes are
+  // summed at the end.  (The same sum as one more MFMA per fragment, ones .
+  // P^T, took config 4 1.035 -> 1.060 ms: 64 MFMA cycles per tile against
+  // 16 VALU instructions.)
+  float lpart[2] = {0.f, 0.f};
   f32x4 o[NDT][2];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
@@ -543,14 +559,14 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) o[dt][qt][r] *= alpha[qt];
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) lacc[qt][r] *= alpha[qt];
+      for (int qt = 0; qt < 2; ++qt) lpart[qt] *= alpha[qt];
     }
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
+    for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj) lacc[qt] = M::run(ones, pf[qt][jj], lacc[qt]);
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) lpart[qt] = M::dot2_ones(pf[qt][jj][e], lpart[qt]);
 
     // O^T += V^T . P^T.  Lane (g, j=c16) addresses V row key0 + 4g + j/4,
     // dims 16dt + 4(j%4) .. +3; rows key0 + 16 and + 32 keep the swizzle, so
@@ -642,7 +658,8 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
   // O = O^T / l, lane l: query tq[qt], dims 16dt + 4g .. +3.
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
-    const float inv = 1.f / lacc[qt][0];  // lt == 0 only if nothing passed: NaN, as the reference
+    // l == 0 only if nothing passed: NaN, as the reference
+    const float inv = 1.f / sum_xor32(sum_xor16(lpart[qt]));
     if (tq[qt] < T) {
       float* orow = a.out + ((b * T + tq[qt]) * HQ + h) * static_cast<int64_t>(D);
 #pragma unroll
