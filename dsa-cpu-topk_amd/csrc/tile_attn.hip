@@ -46,9 +46,9 @@
 // P is rounded to the input's 16-bit type for the second product and for
 // the softmax normaliser, which sums those 16-bit values with v_dot2 against
 // (1, 1) (fp32 accumulation), so numerator and denominator sum the same
-// probabilities (the reference
-// uses fp32 probabilities; the difference is far inside the 16-bit
-// tolerance); everything else is fp32.  Rows that select nothing get
+// probabilities (the reference uses fp32 probabilities; the difference is
+// far inside the 16-bit tolerance); everything else is fp32.  Rows that
+// select nothing get
 // 0/0 = NaN, as the reference.
 #include <mutex>
 #include <type_traits>
@@ -293,9 +293,9 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
   // Softmax normaliser per query: this lane's part, the sum of the 16-bit
   // probabilities of its 16 keys per tile (the values the O product uses),
   // two at a time by v_dot2 against (1, 1); the query's four lanes are
-  // summed at the end.  (The same sum as one more MFMA per fragment, ones .
-  // P^T, took config 4 1.035 -> 1.060 ms: 64 MFMA cycles per tile against
-  // 16 VALU instructions.)
+  // summed at the end.  (Summing with one more MFMA per fragment, ones .
+  // P^T, costs 64 MFMA cycles per wave and tile against these 16 VALU
+  // instructions: config 4 1.060 ms against 1.035 on one box.)
   float lpart[2] = {0.f, 0.f};
   f32x4 o[NDT][2];
 #pragma unroll
