@@ -48,8 +48,7 @@
 // (1, 1) (fp32 accumulation), so numerator and denominator sum the same
 // probabilities (the reference uses fp32 probabilities; the difference is
 // far inside the 16-bit tolerance); everything else is fp32.  Rows that
-// select nothing get
-// 0/0 = NaN, as the reference.
+// select nothing get 0/0 = NaN, as the reference.
 #include <mutex>
 #include <type_traits>
 
