@@ -25,13 +25,16 @@
 // 64-query group, or a chunk of a 64-query group's keys when the batch has
 // fewer groups than the GPU has compute units -- the chunks' partial softmax
 // sums go to a caller-provided workspace and staged_merge_kernel combines
-// them.  What bounds a block (per-block clock traces at config 3): about 25
-// VALU instructions per selected (query, key) pair, so that a group near
-// the start of the row, whose queries select most of their few keys, takes
-// ~200 us for its ~16k pairs; and, on sparse stretches, the copy of each
-// 64 KiB key tile (issued one tile ahead), ~1.8 us per tile.  A tile pair
-// gives every block the same pair count; the groups stream fewer keys in
-// all; the split spreads the long streams when there are not enough blocks.
+// them.  What bounds a block (per-block clock traces at config 3): its
+// selected (query, key) pairs, about 25 VALU instructions each in one
+// dependent chain per pair (8 FMAs, three DPP adds, the max test, exp2, 16
+// accumulator FMAs), with the 4 waves a SIMD holds too few to hide the
+// chain -- as tile pairs every block takes 370-455 us for its ~16k pairs,
+// whether it streams 2080 keys or 4096; a group near the start of the row,
+// whose queries select most of their few keys, takes 150-280 us alone.  A
+// tile pair gives every block the same pair count; the groups stream fewer
+// keys in all; the split spreads the long streams when there are not enough
+// blocks.
 //
 // Measured at config 3 (B=4, T=4096, k=256, HQ=8, D=64, fp32): 0.434-0.44 ms
 // as tile pairs against 0.69-0.75 ms for per-query gathers (as groups 0.47,
