@@ -162,6 +162,14 @@ __device__ __forceinline__ float group_bcast(float v) {
 // Max / sum of v over the lane pairs {l, l^32} and {l, l^16}, on the VALU
 // (v_permlane32_swap / v_permlane16_swap of v with itself: the two results
 // hold, for every lane l, v[l & ~M] and v[l | M], M = 32 or 16).
+// max(x, 0) on the bit pattern: a float with the sign bit set is a negative
+// int32.  One integer max instead of the canonicalising float max the
+// compiler emits for fmaxf on values it cannot prove canonical (MFMA
+// results); -0.0 maps to +0.0, a NaN with the sign bit clear stays NaN.
+__device__ __forceinline__ float relu_f32(float x) {
+  return __int_as_float(max(__float_as_int(x), 0));
+}
+
 __device__ __forceinline__ float max_xor32(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));

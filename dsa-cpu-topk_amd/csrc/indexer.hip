@@ -117,14 +117,6 @@ constexpr size_t kQTileLds = 160 * 1024;  // q + w tile budget per block (all of
 template <typename Tag, int DI>
 constexpr int lane_chunks() { return (DI / 4) * Tag::kBytes / 16; }
 
-// max(x, 0) on the bit pattern: a float with the sign bit set is a negative
-// int32.  One integer max instead of the canonicalising float max the
-// compiler emits for fmaxf on values it cannot prove canonical (MFMA
-// results); -0.0 maps to +0.0, a NaN with the sign bit clear stays NaN.
-__device__ __forceinline__ float relu(float x) {
-  return __int_as_float(max(__float_as_int(x), 0));
-}
-
 // One 16-byte A chunk against the matching chunk of a key block's B slice.
 template <typename Tag, int E>
 __device__ __forceinline__ f32x4 mfma_chunk(const uint4& a, const Slice<Tag, E>& b, int c,
@@ -360,10 +352,10 @@ __global__ __launch_bounds__((64 * qtile_waves<Tag, DI, NQ>())) void indexer_qti
         const float4 wv = wq[(qd * nhg + hg) * 4];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-          sc[qd][kb] = fmaf(wv.x, relu(acc[kb][0]), sc[qd][kb]);
-          sc[qd][kb] = fmaf(wv.y, relu(acc[kb][1]), sc[qd][kb]);
-          sc[qd][kb] = fmaf(wv.z, relu(acc[kb][2]), sc[qd][kb]);
-          sc[qd][kb] = fmaf(wv.w, relu(acc[kb][3]), sc[qd][kb]);
+          sc[qd][kb] = fmaf(wv.x, relu_f32(acc[kb][0]), sc[qd][kb]);
+          sc[qd][kb] = fmaf(wv.y, relu_f32(acc[kb][1]), sc[qd][kb]);
+          sc[qd][kb] = fmaf(wv.z, relu_f32(acc[kb][2]), sc[qd][kb]);
+          sc[qd][kb] = fmaf(wv.w, relu_f32(acc[kb][3]), sc[qd][kb]);
         }
       }
     }

@@ -191,11 +191,13 @@ __device__ __forceinline__ void indexer_rows(const typename Tag::raw* __restrict
           for (int kb = 0; kb < KB; ++kb) acc[kb] = a.mfma(i, bk[kb], acc[kb]);
         }
         __builtin_amdgcn_s_setprio(0);
+        // ReLU on the bit pattern (one integer max; fmaxf on an MFMA result
+        // takes a canonicalising max first): config 1 25.18 -> 24.95 us
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            sc[qg][kb] = fmaf(wv[r], fmaxf(acc[kb][r], 0.f), sc[qg][kb]);
+            sc[qg][kb] = fmaf(wv[r], relu_f32(acc[kb][r]), sc[qg][kb]);
         }
       }
     }

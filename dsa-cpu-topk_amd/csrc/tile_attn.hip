@@ -530,7 +530,19 @@ __global__ __launch_bounds__(kNT, 2) void tile_attn_kernel(TileArgs a) {
             mx = fmaxf(mx, st[j][qt][r]);
           }
       }
-      mx = max_xor32(max_xor16(mx));  // over the 4 lane groups (VALU lane swaps)
+      // over the 4 lane groups (VALU lane swaps).  mx holds no NaN here (the
+      // masked logits' max ignores NaN), so the IEEE maximum gives the same
+      // value with no canonicalising instruction per operand, which fmaxf
+      // needs on exchanged values: 8 VALU instructions fewer per tile
+      // (config 4: 0.970 -> 0.964 ms, the output unchanged).
+      {
+        const auto r16 =
+            __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+        mx = __builtin_elementwise_maximum(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+        const auto r32 =
+            __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+        mx = __builtin_elementwise_maximum(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+      }
       const float m_blk = mx * a.scale_log2;
       const bool up = m_blk > m[qt] + 8.f;
       const float m_new = up ? m_blk : m[qt];
