@@ -281,6 +281,42 @@ def test_threshold_mask_config4_full(dev, k):
     torch.testing.assert_close(thr2[0, rows].cpu(), want_thr, rtol=0, atol=0, equal_nan=True)
 
 
+@pytest.mark.parametrize("T,k,plant", [(12288, 3000, False), (16380, 2048, True),
+                                       (9216, 700, True)])
+def test_threshold_mask_bitmap_path_other_lengths(dev, T, k, plant):
+    """The bitmap form of topk_threshold_mask (rows of 4097-16384 entries) at
+    row counts that are not powers of two -- partial last chunks, between
+    9 and 16 chunks of 1024 entries per row, and causal rows of every length
+    below -- bit for bit against topk_threshold(causal) + selection_mask on
+    every written word; with NaN columns, +-inf and heavy ties planted, or on
+    plain N(0,1) scores, whose rows keep hundreds of values in the sample
+    bracket (the kept-value walks and the wave that finishes the row)."""
+    from dsa_attention import selection_mask
+
+    g = torch.Generator(device=dev).manual_seed(T + k)
+    s = torch.randn((1, T, T), generator=g, device=dev)
+    if plant:
+        s[0, :, ::89] = float("nan")
+        s[0, 5::7, 3::11] = float("inf")
+        s[0, 2::5, 9::13] = float("-inf")
+        s[0, ::6] = torch.randint(0, 4, (T,), generator=g, device=dev).float()
+    s[0].masked_fill_(torch.ones(T, T, dtype=torch.bool, device=dev).triu_(1), 1e30)
+    say(f"topk+mask bitmap path T={T} k={k} plant={plant}")
+    thr2, mask2 = topk_threshold_mask(s, k)
+    thr1 = topk_threshold(s, k, causal=True)
+    mask1 = selection_mask(s, thr1)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(thr2, thr1, rtol=0, atol=0, equal_nan=True)
+    W = (T + 63) // 64
+    t = torch.arange(T, device=dev)
+    written = torch.arange(W, device=dev)[None, :] <= torch.clamp((t | 127) // 64, max=W - 1)[:, None]
+    assert torch.equal(mask2[:, written], mask1[:, written])
+    thr_np = thr2.cpu().numpy()
+    for r in sorted({min(k, T - 1), 4095, 4096, T // 2 + 1, T - 1}):
+        want = mask_words_cpu(s[0, r].cpu().numpy(), r, thr_np[0, r, 0], T)
+        assert np.array_equal(mask2[0, r, : want.size].cpu().numpy(), want), r
+
+
 @pytest.mark.parametrize("k", [1, 100, 2048, 3000, 16383])
 def test_bracket_indices_single_pass(dev, k):
     """Thresholds with exactly-k indices of rows up to 16384 entries come from
